@@ -1,0 +1,135 @@
+/*
+ * tinyserve_moe.h - C ABI of the MI355X (gfx950) fused mixture-of-experts operator.
+ *
+ * Drop-in boundary for tinyserve's qwen3_moe feed-forward block: every entry point here replaces
+ * one function of the reference's Python/Triton MoE path (cited per function, file:line into the
+ * reference tree). Arguments are plain device pointers, sizes and a hipStream_t; there are no torch
+ * types in the signatures. All entry points:
+ *   - are asynchronous on `stream` (no host synchronisation, no device allocation, no memset), so
+ *     they can be captured into a HIP graph;
+ *   - launch a grid whose shape depends only on the sizes, never on the routing;
+ *   - return TSM_OK (0) on success, a negative TSM_E* code on invalid arguments (nothing is launched
+ *     then), or TSM_E_HIP when a launch fails; tsm_last_error() describes the last failure.
+ *
+ * Layouts (row-major, contiguous):
+ *   x       [T, H]       bf16     activations
+ *   gate_w  [E, H]       bf16     router weight (nn.Linear(H, E, bias=False).weight)
+ *   w13     [E, 2I, H]   bf16     rows [0, I) = gate_proj, rows [I, 2I) = up_proj
+ *   w2      [E, H, I]    bf16     down_proj
+ *   topk_w  [T, k]       fp32     routing weights, slot 0 = largest
+ *   topk_ids[T, k]       int32    local expert ids, -1 = expert owned by another GPU
+ */
+#ifndef TINYSERVE_MOE_H
+#define TINYSERVE_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    TSM_OK = 0,
+    TSM_E_ARG = -1,        /* null pointer, negative size, top_k out of range */
+    TSM_E_SHAPE = -2,      /* shape the kernels do not support (e.g. H % 64 != 0) */
+    TSM_E_DTYPE = -3,      /* dtype code not supported by this entry point */
+    TSM_E_WORKSPACE = -4,  /* workspace pointer null/misaligned or smaller than required */
+    TSM_E_HIP = -5         /* a HIP launch failed */
+};
+
+/* dtype codes */
+enum { TSM_F32 = 0, TSM_BF16 = 1 };
+
+/* Description of the last error on the calling thread ("" if none). */
+const char* tsm_last_error(void);
+
+/* ABI version, bumped on any signature change. */
+int tsm_abi_version(void);
+
+/*
+ * Routing from precomputed logits.
+ * Replaces tinykernels.moe_route / _moe_route_kernel (tinykernels.py:1535-1583), and the torch
+ * router branch of SparseMoE.forward (serve.py:1089-1096).
+ * logits: [T, E] with row stride `ld` elements, dtype TSM_F32 or TSM_BF16 (converted exactly to
+ * fp32). Per token: p_e = exp(l_e - max l) in fp32; the top_k largest p are taken largest first,
+ * lowest expert index first among equal p; weights = p / sum(selected p) when renorm != 0, else
+ * p / sum(all p). ids are mapped through expert_map (int64 [E], global -> local id or -1) when it
+ * is non-null. Requires 1 <= top_k <= min(E, 64), E <= 512.
+ */
+int tsm_moe_route(const void* logits, int logits_dtype, int64_t T, int E, int64_t ld, int top_k,
+                  int renorm, const int64_t* expert_map, float* topk_w, int32_t* topk_ids,
+                  hipStream_t stream);
+
+/*
+ * Fused router: gate GEMM (fp32 accumulation with a fixed summation order) + optional per-expert
+ * fp32 bias + optional rounding of the logits to bf16 + the routing of tsm_moe_route, one launch.
+ * Replaces `self.gate(x)` followed by tk.moe_route in SparseMoE.forward (serve.py:1079-1080).
+ * x: [T, H], gate_w: [E, H], both of dtype `dtype` (TSM_BF16 or TSM_F32). bias: [E] fp32 or null.
+ * logits_bf16 != 0 rounds each logit to bf16 (round-to-nearest-even) before the softmax, as the
+ * reference's bf16 nn.Linear output is. logits_out: [T, E] fp32 or null (the logits the softmax
+ * saw). Requires H % 8 == 0, H <= 8192, and the tsm_moe_route limits.
+ */
+int tsm_moe_router(const void* x, const void* gate_w, int dtype, int64_t T, int H, int E,
+                   int top_k, int renorm, const int64_t* expert_map, const float* bias,
+                   int logits_bf16, float* logits_out, float* topk_w, int32_t* topk_ids,
+                   hipStream_t stream);
+
+/*
+ * Block-aligned expert permutation.
+ * Replaces moe_align_block_size (tinykernels.py:1070-1190) and moe_align_block_size_triton
+ * (tinykernels.py:1462-1532); same outputs bit for bit.
+ * ids: [numel] int32 (flattened topk_ids); negative ids go to the remote bucket E.
+ * Outputs: sorted_ids [tsm_moe_max_padded(numel,E,block_m)] int32, expert_ids
+ * [max_padded / block_m] int32, total [1] int32. `ws` is scratch of tsm_moe_align_workspace_size()
+ * bytes (may be null when that size is 0).
+ */
+int64_t tsm_moe_max_padded(int64_t numel, int E, int block_m);
+size_t tsm_moe_align_workspace_size(int64_t numel, int E, int block_m);
+int tsm_moe_align(const int32_t* ids, int64_t numel, int E, int block_m, int32_t* sorted_ids,
+                  int32_t* expert_ids, int32_t* total, void* ws, size_t ws_bytes,
+                  hipStream_t stream);
+
+/*
+ * out[r, :] = bf16( bf16(silu(gate[r, :])) * up[r, :] ), bf16 tensors, strides in elements.
+ * Replaces silu_and_mul / _silu_mul_kernel (tinykernels.py:280-307).
+ */
+int tsm_silu_and_mul(const void* gate, int64_t gate_stride, const void* up, int64_t up_stride,
+                     void* out, int64_t out_stride, int64_t rows, int64_t N, hipStream_t stream);
+
+/*
+ * Tile height (rows per expert tile) fused_moe uses for a batch of T tokens. The reference picks
+ * 16 when T*k <= 4E, else 64 (tinykernels.py:1779); this build picks from its own kernel table.
+ */
+int tsm_moe_block_m(int64_t T, int H, int I, int E, int top_k);
+
+/*
+ * Experts on sorted rows: align + grouped gate_up GEMM with the SwiGLU epilogue + grouped down GEMM
+ * scaled by the routing weight + (sum_topk) the deterministic fixed-order k-sum.
+ * Replaces fused_moe (tinykernels.py:1767-1796) with _moe_gemm/_fused_moe_kernel
+ * (tinykernels.py:1589-1765) and silu_and_mul.
+ * out: [T, H] bf16 when sum_topk != 0, else [T*k, H] bf16 (row t*k+s = weighted expert output of
+ * slot s, zeros for remote slots). Requires H % 64 == 0, I % 64 == 0.
+ */
+size_t tsm_fused_moe_workspace_size(int64_t T, int H, int I, int E, int top_k);
+int tsm_fused_moe(const void* x, const void* w13, const void* w2, const float* topk_w,
+                  const int32_t* topk_ids, int64_t T, int H, int I, int E, int top_k,
+                  int sum_topk, void* out, void* ws, size_t ws_bytes, hipStream_t stream);
+
+/*
+ * Whole SparseMoE.forward on one GPU (serve.py:1076-1087 at TP=1): fused router then fused_moe.
+ * Router options as in tsm_moe_router; topk_w/topk_ids ([T, k]) may be null when the caller does
+ * not need them (they then live in the workspace).
+ */
+size_t tsm_moe_forward_workspace_size(int64_t T, int H, int I, int E, int top_k);
+int tsm_moe_forward(const void* x, const void* gate_w, const void* w13, const void* w2,
+                    const int64_t* expert_map, const float* bias, int64_t T, int H, int I, int E,
+                    int top_k, int renorm, int logits_bf16, int sum_topk, void* out,
+                    float* topk_w, int32_t* topk_ids, void* ws, size_t ws_bytes,
+                    hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* TINYSERVE_MOE_H */

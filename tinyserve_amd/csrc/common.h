@@ -1,0 +1,96 @@
+// Shared device helpers for the gfx950 MoE kernels: bf16 storage, MFMA operand vectors,
+// wavefront reductions, the fp32 exponential the router uses, and error plumbing for the C ABI.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <string.h>
+
+namespace tsm {
+
+typedef uint16_t bf16_t;                                            // bf16 storage (raw bits)
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));          // MFMA A/B operand (8 x bf16)
+typedef float f32x4 __attribute__((ext_vector_type(4)));            // 16x16 MFMA accumulator
+typedef float f32x16 __attribute__((ext_vector_type(16)));          // 32x32 MFMA accumulator
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));         // 16-byte memory chunk
+
+constexpr int kWave = 64;
+
+__device__ __forceinline__ float bf16_to_f32(bf16_t v) {
+    return __uint_as_float(((uint32_t)v) << 16);
+}
+
+// Round to nearest even; NaN stays a quiet NaN. Same rule as torch's float -> bfloat16 cast.
+__host__ __device__ __forceinline__ bf16_t f32_to_bf16(float f) {
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (bf16_t)((u >> 16) | 0x40);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (bf16_t)(u >> 16);
+}
+
+__device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+
+// Low / high bf16 of a packed 32-bit word as fp32 (exact).
+__device__ __forceinline__ float lo_bf16(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float hi_bf16(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
+    return (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
+}
+
+__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+// XOR-butterfly sum over the 64 lanes of a wavefront. Every lane ends with the same value; the
+// addition tree is fixed (partners at distance 32, 16, 8, 4, 2, 1), so the result is deterministic
+// and the host oracle reproduces it bit for bit.
+__device__ __forceinline__ float wave_sum_butterfly(float v) {
+#pragma unroll
+    for (int s = 32; s >= 1; s >>= 1) v += __shfl_xor(v, s);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int s = 32; s >= 1; s >>= 1) v = fmaxf(v, __shfl_xor(v, s));
+    return v;
+}
+
+// exp(x) in fp32 for the router softmax, written out with explicit fmaf so the host oracle
+// (oracle/moe_oracle.c, same algorithm) produces identical bits:
+//   n = rint(x*log2(e)); r = x - n*ln2 (two-constant Cody-Waite reduction, |r| <= ln2/2);
+//   exp(r) by the degree-7 Taylor polynomial in Horner form; result = 2^n * exp(r).
+// Inputs below -86 (including -inf and NaN) return 0, so results are never subnormal.
+__device__ __forceinline__ float router_expf(float x) {
+#pragma clang fp contract(off)
+    if (!(x >= -86.0f)) return 0.0f;
+    if (x > 88.0f) return __builtin_huge_valf();
+    float n = __builtin_rintf(x * 1.44269504088896341f);
+    float r = __builtin_fmaf(-n, 0.693145751953125f, x);
+    r = __builtin_fmaf(-n, 1.42860682030941723e-06f, r);
+    float p = 1.98412698412698413e-04f;  // 1/7!
+    p = __builtin_fmaf(p, r, 1.38888888888888889e-03f);  // 1/6!
+    p = __builtin_fmaf(p, r, 8.33333333333333333e-03f);  // 1/5!
+    p = __builtin_fmaf(p, r, 4.16666666666666667e-02f);  // 1/4!
+    p = __builtin_fmaf(p, r, 1.66666666666666667e-01f);  // 1/3!
+    p = __builtin_fmaf(p, r, 0.5f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    return __builtin_ldexpf(p, (int)n);
+}
+
+}  // namespace tsm
+
+// ---- host-side error plumbing shared by the C-ABI translation units ----
+namespace tsm {
+void set_error(const char* fmt, ...);
+void clear_error();
+int check_launch(const char* what);
+}  // namespace tsm
+
+#define TSM_REQUIRE(cond, code, ...)          \
+    do {                                       \
+        if (!(cond)) {                         \
+            ::tsm::set_error(__VA_ARGS__);     \
+            return (code);                     \
+        }                                      \
+    } while (0)

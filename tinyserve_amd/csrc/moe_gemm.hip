@@ -1,0 +1,448 @@
+// Grouped expert GEMMs on expert-sorted rows, the SwiGLU activation, the fixed-order top-k
+// combine, and the fused_moe / whole-layer entry points.
+//
+// Reference: fused_moe (tinykernels.py:1767-1796) -> _moe_gemm / _fused_moe_kernel
+// (tinykernels.py:1589-1765) twice with silu_and_mul (tinykernels.py:280-307) in between and a
+// torch k-sum at the end; numerics of each row follow the reference: gate/up outputs are rounded
+// to bf16, silu(gate) is rounded to bf16 before the multiply by up, the down output is scaled by
+// the fp32 routing weight and rounded to bf16; the k rows of a token are then summed in fp32.
+//
+// Differences in structure (not in results): the activation is computed in the epilogue of the
+// gate_up GEMM (no [T*k, 2I] intermediate), the activation rows are stored in the expert-sorted
+// order so the down GEMM reads contiguous rows, and the k-sum is a fixed-order pass (slot 0..k-1)
+// rather than a reduction of unspecified order.
+#include <algorithm>
+#include "common.h"
+#include "internal.h"
+#include "tinyserve_moe.h"
+
+namespace tsm {
+namespace {
+
+constexpr int BK = 64;        // K elements per main-loop step
+constexpr int LDK = BK + 8;   // LDS row stride in bf16 elements (144 bytes: 16-byte aligned rows)
+
+struct GemmArgs {
+    const bf16_t* A;            // gate_up: x [T, K]; down: act [max_padded, K]
+    const bf16_t* B;            // gate_up: w13 [E, 2N, K]; down: w2 [E, N, K]
+    bf16_t* C;                  // gate_up: act [max_padded, N]; down: rows [numel, N]
+    const float* topk_w;        // down only: [numel]
+    const int32_t* sorted_ids;  // [max_padded]
+    const int32_t* expert_ids;  // [max_padded / BM]
+    const int32_t* total;       // [1]
+    int64_t numel;
+    int top_k;
+    int N;                      // output columns (gate_up: I; down: H)
+    int K;                      // reduction length (gate_up: H; down: I)
+    int m_tiles;
+    int n_tiles;
+};
+
+// bf16(silu(g)) * u with g, u first rounded to bf16 (the reference stores gate/up as bf16).
+__device__ __forceinline__ float swiglu(float g, float u) {
+    g = round_bf16(g);
+    u = round_bf16(u);
+    const float s = round_bf16(g / (1.0f + __expf(-g)));
+    return s * u;
+}
+
+// Workgroup tile BM x BN of C (for gate_up, BN counts B rows: BN/2 gate rows + the matching BN/2
+// up rows, so BN/2 activation columns), 4 wavefronts in a WM x WN grid, 16x16x32 bf16 MFMA,
+// A and B staged through double-buffered LDS with a register prefetch of the next K step.
+template <int BM, int BN, int WM, int WN, bool GATEUP>
+__global__ __launch_bounds__(256) void moe_gemm_kernel(GemmArgs p) {
+    constexpr int WTM = BM / WM, WTN = BN / WN;
+    constexpr int FM = WTM / 16, FN = WTN / 16;
+    constexpr int A_CHUNKS = BM * (BK / 8), B_CHUNKS = BN * (BK / 8);
+    constexpr int CA = (A_CHUNKS + 255) / 256, CB = B_CHUNKS / 256;
+    static_assert(WM * WN == 4, "4 wavefronts");
+    static_assert(FM >= 1 && FN >= 1 && B_CHUNKS % 256 == 0, "tile shape");
+    static_assert(!GATEUP || FN % 2 == 0, "gate_up wave tile needs gate and up blocks");
+    __shared__ __attribute__((aligned(16))) bf16_t sA[2][BM * LDK];
+    __shared__ __attribute__((aligned(16))) bf16_t sB[2][BN * LDK];
+
+    // XCD-aware tile order: workgroup i runs on XCD i % 8; give each XCD a contiguous range of
+    // logical tiles so that tiles sharing an expert's weight panel meet in the same L2.
+    const int G = p.m_tiles * p.n_tiles;
+    const int pid = blockIdx.x;
+    const int xcd = pid & 7, q = G >> 3, r = G & 7;
+    const int logical = xcd * q + min(xcd, r) + (pid >> 3);
+    const int m_tile = logical % p.m_tiles, n_tile = logical / p.m_tiles;
+    const int m0 = m_tile * BM;
+    if (m0 >= p.total[0]) return;
+    const int expert = p.expert_ids[m_tile];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+
+    if (expert < 0) {  // assignments owned by another GPU: zero rows, no GEMM
+        if (!GATEUP) {
+            for (int idx = tid; idx < BM * (BN / 8); idx += 256) {
+                const int row = idx / (BN / 8), cc = idx % (BN / 8);
+                const int flat = p.sorted_ids[m0 + row];
+                if (flat < p.numel)
+                    *reinterpret_cast<u32x4*>(p.C + (int64_t)flat * p.N + n_tile * BN + cc * 8) =
+                        u32x4{0u, 0u, 0u, 0u};
+            }
+        }
+        return;
+    }
+
+    const bf16_t* a_src[CA];
+#pragma unroll
+    for (int c = 0; c < CA; ++c) {
+        const int idx = tid + c * 256;
+        const bf16_t* s = nullptr;
+        if (idx < A_CHUNKS) {
+            const int row = idx / (BK / 8), kc = idx % (BK / 8);
+            if (GATEUP) {
+                const int flat = p.sorted_ids[m0 + row];
+                if (flat < p.numel) s = p.A + (int64_t)(flat / p.top_k) * p.K + kc * 8;
+            } else {
+                s = p.A + (int64_t)(m0 + row) * p.K + kc * 8;
+            }
+        }
+        a_src[c] = s;
+    }
+    const bf16_t* Be = p.B + (int64_t)expert * (GATEUP ? 2 : 1) * p.N * p.K;
+    const bf16_t* b_src[CB];
+#pragma unroll
+    for (int c = 0; c < CB; ++c) {
+        const int idx = tid + c * 256;
+        const int row = idx / (BK / 8), kc = idx % (BK / 8);
+        int brow;
+        if (GATEUP)
+            brow = row < BN / 2 ? n_tile * (BN / 2) + row : p.N + n_tile * (BN / 2) + row - BN / 2;
+        else
+            brow = n_tile * BN + row;
+        b_src[c] = Be + (int64_t)brow * p.K + kc * 8;
+    }
+
+    u32x4 ra[CA], rb[CB];
+    auto gload = [&](int kt) {
+#pragma unroll
+        for (int c = 0; c < CA; ++c)
+            ra[c] = a_src[c] ? *reinterpret_cast<const u32x4*>(a_src[c] + kt * BK)
+                             : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int c = 0; c < CB; ++c) rb[c] = *reinterpret_cast<const u32x4*>(b_src[c] + kt * BK);
+    };
+    auto sstore = [&](int buf) {
+#pragma unroll
+        for (int c = 0; c < CA; ++c) {
+            const int idx = tid + c * 256;
+            if (idx < A_CHUNKS) {
+                const int row = idx / (BK / 8), kc = idx % (BK / 8);
+                *reinterpret_cast<u32x4*>(&sA[buf][row * LDK + kc * 8]) = ra[c];
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < CB; ++c) {
+            const int idx = tid + c * 256;
+            const int row = idx / (BK / 8), kc = idx % (BK / 8);
+            *reinterpret_cast<u32x4*>(&sB[buf][row * LDK + kc * 8]) = rb[c];
+        }
+    };
+
+    const int wm = wave / WN, wn = wave % WN;
+    constexpr int OW = WTN / 2;  // gate_up: activation columns per wavefront
+    auto brow_of = [&](int g) {
+        if (GATEUP)
+            return g < FN / 2 ? wn * OW + g * 16 : BN / 2 + wn * OW + (g - FN / 2) * 16;
+        return wn * WTN + g * 16;
+    };
+
+    f32x4 acc[FM][FN];
+#pragma unroll
+    for (int f = 0; f < FM; ++f)
+#pragma unroll
+        for (int g = 0; g < FN; ++g) acc[f][g] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    const int KT = p.K / BK;
+    gload(0);
+    sstore(0);
+    __syncthreads();
+    for (int kt = 0; kt < KT; ++kt) {
+        const int buf = kt & 1;
+        if (kt + 1 < KT) gload(kt + 1);
+#pragma unroll
+        for (int ks = 0; ks < BK / 32; ++ks) {
+            const int koff = ks * 32 + (lane >> 4) * 8;
+            bf16x8 af[FM], bfr[FN];
+#pragma unroll
+            for (int f = 0; f < FM; ++f) {
+                const int row = wm * WTM + f * 16 + (lane & 15);
+                af[f] = as_bf16x8(*reinterpret_cast<const u32x4*>(&sA[buf][row * LDK + koff]));
+            }
+#pragma unroll
+            for (int g = 0; g < FN; ++g) {
+                const int row = brow_of(g) + (lane & 15);
+                bfr[g] = as_bf16x8(*reinterpret_cast<const u32x4*>(&sB[buf][row * LDK + koff]));
+            }
+#pragma unroll
+            for (int f = 0; f < FM; ++f)
+#pragma unroll
+                for (int g = 0; g < FN; ++g)
+                    acc[f][g] =
+                        __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[f], bfr[g], acc[f][g], 0, 0, 0);
+        }
+        if (kt + 1 < KT) sstore(buf ^ 1);
+        __syncthreads();
+    }
+
+    // Epilogue. Accumulator element i of block (f, g) is row (lane/16)*4 + i, column lane%16.
+#pragma unroll
+    for (int f = 0; f < FM; ++f) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int grow = m0 + wm * WTM + f * 16 + (lane >> 4) * 4 + i;
+            if (GATEUP) {
+#pragma unroll
+                for (int g = 0; g < FN / 2; ++g) {
+                    const int col = n_tile * (BN / 2) + wn * OW + g * 16 + (lane & 15);
+                    p.C[(int64_t)grow * p.N + col] =
+                        f32_to_bf16(swiglu(acc[f][g][i], acc[f][g + FN / 2][i]));
+                }
+            } else {
+                const int flat = p.sorted_ids[grow];
+                if (flat < p.numel) {
+                    const float w = p.topk_w[flat];
+#pragma unroll
+                    for (int g = 0; g < FN; ++g) {
+                        const int col = n_tile * BN + wn * WTN + g * 16 + (lane & 15);
+                        p.C[(int64_t)flat * p.N + col] = f32_to_bf16(acc[f][g][i] * w);
+                    }
+                }
+            }
+        }
+    }
+}
+
+// out[t, :] = bf16(sum over s = 0..k-1 of rows[t*k + s, :]) with fp32 accumulation in slot order.
+__global__ __launch_bounds__(256) void combine_kernel(const bf16_t* __restrict__ rows,
+                                                      bf16_t* __restrict__ out, int64_t T, int H,
+                                                      int k) {
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int cpr = H / 8;
+    const int64_t t = idx / cpr;
+    const int c = (int)(idx % cpr);
+    if (t >= T) return;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int s = 0; s < k; ++s) {
+        const u32x4 v = *reinterpret_cast<const u32x4*>(rows + ((t * k + s) * H + c * 8));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            acc[2 * j] += lo_bf16(v[j]);
+            acc[2 * j + 1] += hi_bf16(v[j]);
+        }
+    }
+    u32x4 o;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o[j] = pack_bf16(acc[2 * j], acc[2 * j + 1]);
+    *reinterpret_cast<u32x4*>(out + (t * H + c * 8)) = o;
+}
+
+__global__ __launch_bounds__(256) void silu_mul_kernel(const bf16_t* __restrict__ gate,
+                                                       int64_t gs, const bf16_t* __restrict__ up,
+                                                       int64_t us, bf16_t* __restrict__ out,
+                                                       int64_t os, int64_t N) {
+    const int64_t row = blockIdx.y;
+    for (int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x; c < N;
+         c += (int64_t)gridDim.x * 256) {
+        const float g = bf16_to_f32(gate[row * gs + c]);
+        const float u = bf16_to_f32(up[row * us + c]);
+        const float s = round_bf16(g / (1.0f + __expf(-g)));
+        out[row * os + c] = f32_to_bf16(s * u);
+    }
+}
+
+// ---- kernel table --------------------------------------------------------------------------
+enum Variant { kDecode = 0, kPrefill = 1 };
+
+struct Plan {
+    int block_m;
+    Variant v;
+};
+
+Plan plan_for(int64_t T, int E, int top_k) {
+    const int64_t numel = T * top_k;
+    if (numel <= 4ll * E) return Plan{16, kDecode};
+    return Plan{64, kPrefill};
+}
+
+template <int BM, int BN, int WM, int WN>
+hipError_t launch_pair(const GemmArgs& g1, const GemmArgs& g2, hipStream_t stream) {
+    hipLaunchKernelGGL((moe_gemm_kernel<BM, BN, WM, WN, true>), dim3(g1.m_tiles * g1.n_tiles),
+                       dim3(256), 0, stream, g1);
+    hipLaunchKernelGGL((moe_gemm_kernel<BM, BN, WM, WN, false>), dim3(g2.m_tiles * g2.n_tiles),
+                       dim3(256), 0, stream, g2);
+    return hipGetLastError();
+}
+
+constexpr int kBN = 128;  // B rows per workgroup tile (both variants)
+
+struct Layout {
+    size_t sorted, expert_ids, total, hist, act, rows, topk_w, topk_ids, bytes;
+};
+
+Layout layout_for(int64_t T, int H, int I, int E, int top_k, bool with_route) {
+    const Plan pl = plan_for(T, E, top_k);
+    const int64_t numel = T * top_k;
+    const int64_t mp = max_padded_rows(numel, E, pl.block_m);
+    Layout L{};
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        const size_t at = off;
+        off = align_up(off + bytes, 256);
+        return at;
+    };
+    L.sorted = take(sizeof(int32_t) * mp);
+    L.expert_ids = take(sizeof(int32_t) * (mp / pl.block_m));
+    L.total = take(sizeof(int32_t));
+    L.hist = take(align_workspace_bytes(numel, E));
+    L.act = take(sizeof(bf16_t) * mp * I);
+    L.rows = take(sizeof(bf16_t) * numel * H);
+    if (with_route) {
+        L.topk_w = take(sizeof(float) * numel);
+        L.topk_ids = take(sizeof(int32_t) * numel);
+    }
+    L.bytes = off;
+    return L;
+}
+
+int check_moe_shapes(int64_t T, int H, int I, int E, int top_k) {
+    TSM_REQUIRE(T >= 0 && T < (1ll << 24), TSM_E_ARG, "T out of range (%lld)", (long long)T);
+    TSM_REQUIRE(H >= 64 && H % kBN == 0, TSM_E_SHAPE, "H must be a positive multiple of %d (got %d)",
+                kBN, H);
+    TSM_REQUIRE(I >= 64 && I % (kBN / 2) == 0, TSM_E_SHAPE,
+                "I must be a positive multiple of %d (got %d)", kBN / 2, I);
+    TSM_REQUIRE(top_k >= 1 && top_k <= 64, TSM_E_ARG, "top_k must be in [1, 64] (got %d)", top_k);
+    return check_align_args(T * top_k, E, 64);
+}
+
+// Everything after routing: align, gate_up + SwiGLU, down * weight, k-sum.
+int run_experts(const void* x, const void* w13, const void* w2, const float* topk_w,
+                const int32_t* topk_ids, int64_t T, int H, int I, int E, int top_k, int sum_topk,
+                void* out, char* ws, const Layout& L, hipStream_t stream) {
+    const Plan pl = plan_for(T, E, top_k);
+    const int64_t numel = T * top_k;
+    const int64_t mp = max_padded_rows(numel, E, pl.block_m);
+    int32_t* sorted = reinterpret_cast<int32_t*>(ws + L.sorted);
+    int32_t* eids = reinterpret_cast<int32_t*>(ws + L.expert_ids);
+    int32_t* total = reinterpret_cast<int32_t*>(ws + L.total);
+    bf16_t* act = reinterpret_cast<bf16_t*>(ws + L.act);
+    bf16_t* rows = sum_topk ? reinterpret_cast<bf16_t*>(ws + L.rows) : (bf16_t*)out;
+
+    (void)launch_align(topk_ids, numel, E, pl.block_m, sorted, eids, total, ws + L.hist, stream);
+
+    GemmArgs g1{};
+    g1.A = (const bf16_t*)x;
+    g1.B = (const bf16_t*)w13;
+    g1.C = act;
+    g1.topk_w = topk_w;
+    g1.sorted_ids = sorted;
+    g1.expert_ids = eids;
+    g1.total = total;
+    g1.numel = numel;
+    g1.top_k = top_k;
+    g1.N = I;
+    g1.K = H;
+    g1.m_tiles = (int)(mp / pl.block_m);
+    g1.n_tiles = I / (kBN / 2);
+    GemmArgs g2 = g1;
+    g2.A = act;
+    g2.B = (const bf16_t*)w2;
+    g2.C = rows;
+    g2.N = H;
+    g2.K = I;
+    g2.n_tiles = H / kBN;
+    if (pl.v == kDecode)
+        (void)launch_pair<16, kBN, 1, 4>(g1, g2, stream);
+    else
+        (void)launch_pair<64, kBN, 2, 2>(g1, g2, stream);
+
+    if (sum_topk) {
+        const int64_t threads = T * (H / 8);
+        hipLaunchKernelGGL(combine_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
+                           stream, rows, (bf16_t*)out, T, H, top_k);
+    }
+    return check_launch("fused_moe kernels");
+}
+
+}  // namespace
+}  // namespace tsm
+
+using namespace tsm;
+
+extern "C" int tsm_moe_block_m(int64_t T, int H, int I, int E, int top_k) {
+    (void)H;
+    (void)I;
+    return plan_for(T, E, top_k).block_m;
+}
+
+extern "C" int tsm_silu_and_mul(const void* gate, int64_t gate_stride, const void* up,
+                                int64_t up_stride, void* out, int64_t out_stride, int64_t rows,
+                                int64_t N, hipStream_t stream) {
+    clear_error();
+    TSM_REQUIRE(rows >= 0 && N >= 0 && rows < 65536ll * 1024, TSM_E_ARG, "bad sizes");
+    if (rows == 0 || N == 0) return TSM_OK;
+    TSM_REQUIRE(gate && up && out, TSM_E_ARG, "null pointer argument");
+    const unsigned gx = (unsigned)std::min<int64_t>((N + 255) / 256, 64);
+    // gridDim.y is limited to 65535: process rows in bands
+    for (int64_t r0 = 0; r0 < rows; r0 += 65535) {
+        const int64_t nr = std::min<int64_t>(65535, rows - r0);
+        hipLaunchKernelGGL(silu_mul_kernel, dim3(gx, (unsigned)nr), dim3(256), 0, stream,
+                           (const bf16_t*)gate + r0 * gate_stride, gate_stride,
+                           (const bf16_t*)up + r0 * up_stride, up_stride,
+                           (bf16_t*)out + r0 * out_stride, out_stride, N);
+    }
+    return check_launch("silu_mul_kernel");
+}
+
+extern "C" size_t tsm_fused_moe_workspace_size(int64_t T, int H, int I, int E, int top_k) {
+    if (T < 0 || H <= 0 || I <= 0 || E <= 0 || top_k <= 0) return 0;
+    return layout_for(T, H, I, E, top_k, false).bytes;
+}
+
+extern "C" int tsm_fused_moe(const void* x, const void* w13, const void* w2, const float* topk_w,
+                             const int32_t* topk_ids, int64_t T, int H, int I, int E, int top_k,
+                             int sum_topk, void* out, void* ws, size_t ws_bytes,
+                             hipStream_t stream) {
+    clear_error();
+    int rc = check_moe_shapes(T, H, I, E, top_k);
+    if (rc) return rc;
+    if (T == 0) return TSM_OK;
+    TSM_REQUIRE(x && w13 && w2 && topk_w && topk_ids && out, TSM_E_ARG, "null pointer argument");
+    const Layout L = layout_for(T, H, I, E, top_k, false);
+    TSM_REQUIRE(ws && ws_bytes >= L.bytes && ((uintptr_t)ws & 255) == 0, TSM_E_WORKSPACE,
+                "workspace must be 256-byte aligned and >= %zu bytes (got %zu)", L.bytes,
+                ws_bytes);
+    return run_experts(x, w13, w2, topk_w, topk_ids, T, H, I, E, top_k, sum_topk, out,
+                       (char*)ws, L, stream);
+}
+
+extern "C" size_t tsm_moe_forward_workspace_size(int64_t T, int H, int I, int E, int top_k) {
+    if (T < 0 || H <= 0 || I <= 0 || E <= 0 || top_k <= 0) return 0;
+    return layout_for(T, H, I, E, top_k, true).bytes;
+}
+
+extern "C" int tsm_moe_forward(const void* x, const void* gate_w, const void* w13, const void* w2,
+                               const int64_t* expert_map, const float* bias, int64_t T, int H,
+                               int I, int E, int top_k, int renorm, int logits_bf16,
+                               int sum_topk, void* out, float* topk_w, int32_t* topk_ids,
+                               void* ws, size_t ws_bytes, hipStream_t stream) {
+    clear_error();
+    int rc = check_moe_shapes(T, H, I, E, top_k);
+    if (rc) return rc;
+    if (T == 0) return TSM_OK;
+    TSM_REQUIRE(x && gate_w && w13 && w2 && out, TSM_E_ARG, "null pointer argument");
+    const Layout L = layout_for(T, H, I, E, top_k, true);
+    TSM_REQUIRE(ws && ws_bytes >= L.bytes && ((uintptr_t)ws & 255) == 0, TSM_E_WORKSPACE,
+                "workspace must be 256-byte aligned and >= %zu bytes (got %zu)", L.bytes,
+                ws_bytes);
+    char* w = (char*)ws;
+    float* tw = topk_w ? topk_w : reinterpret_cast<float*>(w + L.topk_w);
+    int32_t* ti = topk_ids ? topk_ids : reinterpret_cast<int32_t*>(w + L.topk_ids);
+    rc = tsm_moe_router(x, gate_w, TSM_BF16, T, H, E, top_k, renorm, expert_map, bias,
+                        logits_bf16, nullptr, tw, ti, stream);
+    if (rc) return rc;
+    return run_experts(x, w13, w2, tw, ti, T, H, I, E, top_k, sum_topk, out, w, L, stream);
+}

@@ -1,0 +1,298 @@
+// Router kernels: fp32 softmax + top-k + renormalisation, one wavefront per token, optionally
+// preceded by the router (gate) GEMM in the same launch.
+//
+// Reference behaviour: _moe_route_kernel / moe_route (tinykernels.py:1535-1583) and the torch router
+// branch of SparseMoE.forward (serve.py:1089-1096). Selection is on p = exp(l - max l) with the
+// lowest expert index winning ties, as the Triton kernel's first-index argmax does; weights are
+// p / sum(selected p) (renormalise) or p / sum(all p).
+//
+// Every floating-point operation on this path has a fixed order and uses router_expf, so the
+// logits, ids and weights are reproducible bit for bit by a sequential host program:
+//   logit(t, e): lane j of a wavefront accumulates, with fmaf starting from +0, the products
+//   x[t,h]*g[e,h] for h = c*512 + j*8 + i in increasing (c, i) order (h < H); the 64 lane partials are
+//   then summed by the XOR butterfly of wave_sum_butterfly; bias[e] is added if given; the result is
+//   rounded to bf16 if requested.
+#include "common.h"
+#include "tinyserve_moe.h"
+
+namespace tsm {
+namespace {
+
+constexpr int kMaxM = 8;          // experts per lane: E <= 512
+constexpr int kRouterWaves = 16;  // wavefronts per router workgroup
+
+// Softmax numerators, top-k and weights for one token whose logits lane j holds at
+// v[q] = logit[j + 64 q]. Writes topk_w/topk_ids[0..k). All lanes of the wavefront must call it.
+__device__ __forceinline__ void wave_select(float (&v)[kMaxM], int E, int top_k, int renorm,
+                                            const int64_t* __restrict__ expert_map,
+                                            float* __restrict__ out_w,
+                                            int32_t* __restrict__ out_ids) {
+#pragma clang fp contract(off)
+    const int lane = threadIdx.x & (kWave - 1);
+    float m = -__builtin_huge_valf();
+#pragma unroll
+    for (int q = 0; q < kMaxM; ++q)
+        if (lane + 64 * q < E) m = fmaxf(m, v[q]);
+    m = wave_max(m);
+
+    float part = 0.0f;  // this lane's share of sum(p), ascending q
+#pragma unroll
+    for (int q = 0; q < kMaxM; ++q) {
+        if (lane + 64 * q < E) {
+            v[q] = router_expf(v[q] - m);
+            part = part + v[q];
+        } else {
+            v[q] = -__builtin_huge_valf();
+        }
+    }
+
+    float sel_sum = 0.0f, my_v = 0.0f;
+    int my_i = 0;
+    for (int s = 0; s < top_k; ++s) {
+        float bv = -__builtin_huge_valf();
+        int bi = 0x7fffffff;
+#pragma unroll
+        for (int q = 0; q < kMaxM; ++q)
+            if (v[q] > bv) { bv = v[q]; bi = lane + 64 * q; }
+#pragma unroll
+        for (int sh = 32; sh >= 1; sh >>= 1) {
+            float ov = __shfl_xor(bv, sh);
+            int oi = __shfl_xor(bi, sh);
+            if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+        }
+        sel_sum = sel_sum + bv;
+        if (lane == s) { my_v = bv; my_i = bi; }
+#pragma unroll
+        for (int q = 0; q < kMaxM; ++q)
+            if (bi == lane + 64 * q) v[q] = -__builtin_huge_valf();
+    }
+    float denom = renorm ? sel_sum : wave_sum_butterfly(part);
+    if (lane < top_k) {
+        out_w[lane] = my_v / denom;
+        out_ids[lane] = expert_map ? (int32_t)expert_map[my_i] : (int32_t)my_i;
+    }
+}
+
+template <typename TLog>
+__device__ __forceinline__ float load_logit(const TLog* p, int64_t i);
+template <>
+__device__ __forceinline__ float load_logit<float>(const float* p, int64_t i) { return p[i]; }
+template <>
+__device__ __forceinline__ float load_logit<bf16_t>(const bf16_t* p, int64_t i) {
+    return bf16_to_f32(p[i]);
+}
+
+// One wavefront per token; 4 tokens per 256-thread workgroup.
+template <typename TLog>
+__global__ __launch_bounds__(256) void route_logits_kernel(
+    const TLog* __restrict__ logits, int64_t T, int E, int64_t ld, int top_k, int renorm,
+    const int64_t* __restrict__ expert_map, float* __restrict__ topk_w,
+    int32_t* __restrict__ topk_ids) {
+    const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= T) return;
+    const int lane = threadIdx.x & 63;
+    float v[kMaxM];
+#pragma unroll
+    for (int q = 0; q < kMaxM; ++q) {
+        int e = lane + 64 * q;
+        v[q] = e < E ? load_logit<TLog>(logits, t * ld + e) : 0.0f;
+    }
+    wave_select(v, E, top_k, renorm, expert_map, topk_w + t * top_k, topk_ids + t * top_k);
+}
+
+// Eight consecutive inputs starting at p (16-byte aligned for bf16, 32-byte for fp32) as fp32.
+__device__ __forceinline__ void load8(const bf16_t* p, float (&o)[8]) {
+    u32x4 w = *reinterpret_cast<const u32x4*>(p);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { o[2 * i] = lo_bf16(w[i]); o[2 * i + 1] = hi_bf16(w[i]); }
+}
+__device__ __forceinline__ void load8(const float* p, float (&o)[8]) {
+    float4 a = reinterpret_cast<const float4*>(p)[0];
+    float4 b = reinterpret_cast<const float4*>(p)[1];
+    o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w; o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
+}
+
+// Gate GEMM + routing. Workgroup = kRouterWaves wavefronts and TB tokens; each wavefront computes
+// the logits of experts e = wave, wave + kRouterWaves, ... for the TB tokens (x slice held in
+// registers as fp32, the gate row streamed from L2 with one 16-byte load per lane per 512
+// columns), then wavefronts 0..TB-1 run the selection on the LDS logits of one token each.
+template <typename TIn, int NC, int TB>
+__global__ __launch_bounds__(kRouterWaves * 64) void router_kernel(
+    const TIn* __restrict__ x, const TIn* __restrict__ gw, int64_t T, int H, int E, int top_k,
+    int renorm, const int64_t* __restrict__ expert_map, const float* __restrict__ bias,
+    int logits_bf16, float* __restrict__ logits_out, float* __restrict__ topk_w,
+    int32_t* __restrict__ topk_ids) {
+#pragma clang fp contract(off)
+    extern __shared__ float s_logits[];  // [TB][E]
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int64_t t0 = (int64_t)blockIdx.x * TB;
+
+    float xr[TB][NC * 8];
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb) {
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            const int h0 = c * 512 + lane * 8;
+            float tmp[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+            if (h0 < H && t0 + tb < T) load8(x + (t0 + tb) * H + h0, tmp);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) xr[tb][c * 8 + i] = tmp[i];
+        }
+    }
+
+    for (int e = wave; e < E; e += kRouterWaves) {
+        float g[NC * 8];
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            const int h0 = c * 512 + lane * 8;
+            float tmp[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+            if (h0 < H) load8(gw + (int64_t)e * H + h0, tmp);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) g[c * 8 + i] = tmp[i];
+        }
+#pragma unroll
+        for (int tb = 0; tb < TB; ++tb) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+                if (c * 512 + lane * 8 < H) {
+#pragma unroll
+                    for (int i = 0; i < 8; ++i)
+                        acc = __builtin_fmaf(xr[tb][c * 8 + i], g[c * 8 + i], acc);
+                }
+            }
+            float l = wave_sum_butterfly(acc);
+            if (bias) l = l + bias[e];
+            if (logits_bf16) l = round_bf16(l);
+            if (lane == 0) {
+                s_logits[tb * E + e] = l;
+                if (logits_out && t0 + tb < T) logits_out[(t0 + tb) * E + e] = l;
+            }
+        }
+    }
+    __syncthreads();
+
+    for (int tb = wave; tb < TB; tb += kRouterWaves) {
+        const int64_t t = t0 + tb;
+        if (t >= T) break;
+        float v[kMaxM];
+#pragma unroll
+        for (int q = 0; q < kMaxM; ++q) {
+            int e = lane + 64 * q;
+            v[q] = e < E ? s_logits[tb * E + e] : 0.0f;
+        }
+        wave_select(v, E, top_k, renorm, expert_map, topk_w + t * top_k, topk_ids + t * top_k);
+    }
+}
+
+template <typename TIn, int NC, int TB>
+hipError_t launch_router_tb(const void* x, const void* gw, int64_t T, int H, int E, int top_k,
+                            int renorm, const int64_t* expert_map, const float* bias,
+                            int logits_bf16, float* logits_out, float* w, int32_t* ids,
+                            hipStream_t stream) {
+    const int64_t blocks = (T + TB - 1) / TB;
+    const size_t lds = sizeof(float) * TB * E;
+    hipLaunchKernelGGL((router_kernel<TIn, NC, TB>), dim3((unsigned)blocks),
+                       dim3(kRouterWaves * 64), lds, stream, (const TIn*)x, (const TIn*)gw, T, H,
+                       E, top_k, renorm, expert_map, bias, logits_bf16, logits_out, w, ids);
+    return hipGetLastError();
+}
+
+// Tokens per workgroup: one for decode-sized batches (more workgroups, lower latency); for larger
+// batches as many as keep the x slice within 64 fp32 registers per lane.
+template <typename TIn, int NC>
+hipError_t launch_router_nc(const void* x, const void* gw, int64_t T, int H, int E, int top_k,
+                            int renorm, const int64_t* expert_map, const float* bias,
+                            int logits_bf16, float* logits_out, float* w, int32_t* ids,
+                            hipStream_t stream) {
+    constexpr int TBMAX = (8 / NC) > 0 ? (8 / NC) : 1;
+    if (T <= 256 || TBMAX == 1)
+        return launch_router_tb<TIn, NC, 1>(x, gw, T, H, E, top_k, renorm, expert_map, bias,
+                                            logits_bf16, logits_out, w, ids, stream);
+    return launch_router_tb<TIn, NC, TBMAX>(x, gw, T, H, E, top_k, renorm, expert_map, bias,
+                                            logits_bf16, logits_out, w, ids, stream);
+}
+
+template <typename TIn>
+hipError_t launch_router(const void* x, const void* gw, int64_t T, int H, int E, int top_k,
+                         int renorm, const int64_t* expert_map, const float* bias,
+                         int logits_bf16, float* logits_out, float* w, int32_t* ids,
+                         hipStream_t stream) {
+    const int nc = (H + 511) / 512;
+#define TSM_ROUTER_NC(N)                                                                         \
+    if (nc <= N)                                                                                 \
+        return launch_router_nc<TIn, N>(x, gw, T, H, E, top_k, renorm, expert_map, bias,        \
+                                        logits_bf16, logits_out, w, ids, stream);
+    TSM_ROUTER_NC(1)
+    TSM_ROUTER_NC(2)
+    TSM_ROUTER_NC(4)
+    TSM_ROUTER_NC(8)
+#undef TSM_ROUTER_NC
+    return hipErrorInvalidValue;
+}
+
+int check_route_args(int64_t T, int E, int top_k) {
+    TSM_REQUIRE(T >= 0, TSM_E_ARG, "T must be >= 0 (got %lld)", (long long)T);
+    TSM_REQUIRE(E >= 1 && E <= 64 * kMaxM, TSM_E_SHAPE, "E must be in [1, %d] (got %d)",
+                64 * kMaxM, E);
+    TSM_REQUIRE(top_k >= 1 && top_k <= E && top_k <= 64, TSM_E_ARG,
+                "top_k must be in [1, min(E, 64)] (got %d, E=%d)", top_k, E);
+    return TSM_OK;
+}
+
+}  // namespace
+}  // namespace tsm
+
+using namespace tsm;
+
+extern "C" int tsm_moe_route(const void* logits, int logits_dtype, int64_t T, int E, int64_t ld,
+                             int top_k, int renorm, const int64_t* expert_map, float* topk_w,
+                             int32_t* topk_ids, hipStream_t stream) {
+    clear_error();
+    int rc = check_route_args(T, E, top_k);
+    if (rc) return rc;
+    TSM_REQUIRE(ld >= E, TSM_E_ARG, "ld (%lld) must be >= E (%d)", (long long)ld, E);
+    if (T == 0) return TSM_OK;
+    TSM_REQUIRE(logits && topk_w && topk_ids, TSM_E_ARG, "null pointer argument");
+    const unsigned blocks = (unsigned)((T + 3) / 4);
+    if (logits_dtype == TSM_F32) {
+        hipLaunchKernelGGL(route_logits_kernel<float>, dim3(blocks), dim3(256), 0, stream,
+                           (const float*)logits, T, E, ld, top_k, renorm, expert_map, topk_w,
+                           topk_ids);
+    } else if (logits_dtype == TSM_BF16) {
+        hipLaunchKernelGGL(route_logits_kernel<bf16_t>, dim3(blocks), dim3(256), 0, stream,
+                           (const bf16_t*)logits, T, E, ld, top_k, renorm, expert_map, topk_w,
+                           topk_ids);
+    } else {
+        set_error("logits dtype code %d not supported", logits_dtype);
+        return TSM_E_DTYPE;
+    }
+    return check_launch("route_logits_kernel");
+}
+
+extern "C" int tsm_moe_router(const void* x, const void* gate_w, int dtype, int64_t T, int H,
+                              int E, int top_k, int renorm, const int64_t* expert_map,
+                              const float* bias, int logits_bf16, float* logits_out,
+                              float* topk_w, int32_t* topk_ids, hipStream_t stream) {
+    clear_error();
+    int rc = check_route_args(T, E, top_k);
+    if (rc) return rc;
+    TSM_REQUIRE(H >= 8 && H % 8 == 0 && H <= 4096, TSM_E_SHAPE,
+                "router needs H %% 8 == 0 and 8 <= H <= 4096 (got %d)", H);
+    if (T == 0) return TSM_OK;
+    TSM_REQUIRE(x && gate_w && topk_w && topk_ids, TSM_E_ARG, "null pointer argument");
+    hipError_t err;
+    if (dtype == TSM_BF16)
+        err = launch_router<bf16_t>(x, gate_w, T, H, E, top_k, renorm, expert_map, bias,
+                                    logits_bf16, logits_out, topk_w, topk_ids, stream);
+    else if (dtype == TSM_F32)
+        err = launch_router<float>(x, gate_w, T, H, E, top_k, renorm, expert_map, bias,
+                                   logits_bf16, logits_out, topk_w, topk_ids, stream);
+    else {
+        set_error("router dtype code %d not supported", dtype);
+        return TSM_E_DTYPE;
+    }
+    (void)err;
+    return check_launch("router_kernel");
+}

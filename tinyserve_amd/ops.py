@@ -1,0 +1,221 @@
+"""PyTorch custom ops (namespace `tinyserve_amd`) over the C ABI of libtinyserve_moe.so.
+
+Every op validates shapes/dtypes/devices here, allocates its outputs and workspace with torch's
+caching allocator, and launches on torch's current stream; nothing synchronises the host, so the
+ops can be captured into a HIP graph (torch.cuda.graph). There is no CPU implementation: a CPU
+tensor raises.
+"""
+from typing import Optional, Tuple
+
+import torch
+from torch import Tensor
+
+from ._lib import TSM_BF16, TSM_F32, check, lib, ptr, stream_of
+
+
+def _on_gpu(*tensors):
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise RuntimeError(
+                f"tinyserve_amd ops run on the GPU only (got a tensor on {t.device}); "
+                "there is no CPU implementation")
+
+
+def _contig(t: Tensor) -> Tensor:
+    return t if t.is_contiguous() else t.contiguous()
+
+
+def _map_arg(expert_map: Optional[Tensor], device) -> Optional[Tensor]:
+    if expert_map is None:
+        return None
+    return _contig(expert_map.to(device=device, dtype=torch.int64))
+
+
+# ---------------------------------------------------------------- routing
+@torch.library.custom_op("tinyserve_amd::moe_route", mutates_args=())
+def moe_route(logits: Tensor, top_k: int, renormalize: bool,
+              expert_map: Optional[Tensor] = None) -> Tuple[Tensor, Tensor]:
+    """logits [T, E] -> (topk_weights fp32 [T, k], topk_ids int32 [T, k])."""
+    _on_gpu(logits, expert_map)
+    if logits.dim() != 2:
+        raise ValueError(f"logits must be [T, E], got {tuple(logits.shape)}")
+    if logits.dtype not in (torch.float32, torch.bfloat16):
+        logits = logits.float()
+    if logits.stride(1) != 1:
+        logits = logits.contiguous()
+    T, E = logits.shape
+    w = torch.empty(T, top_k, dtype=torch.float32, device=logits.device)
+    ids = torch.empty(T, top_k, dtype=torch.int32, device=logits.device)
+    m = _map_arg(expert_map, logits.device)
+    dt = TSM_F32 if logits.dtype == torch.float32 else TSM_BF16
+    check(lib.tsm_moe_route(ptr(logits), dt, T, E, logits.stride(0), top_k, int(renormalize),
+                            ptr(m), ptr(w), ptr(ids), stream_of(logits)), "moe_route")
+    return w, ids
+
+
+@moe_route.register_fake
+def _(logits, top_k, renormalize, expert_map=None):
+    T = logits.shape[0]
+    return (logits.new_empty(T, top_k, dtype=torch.float32),
+            logits.new_empty(T, top_k, dtype=torch.int32))
+
+
+@torch.library.custom_op("tinyserve_amd::moe_router", mutates_args=())
+def moe_router(x: Tensor, gate_w: Tensor, top_k: int, renormalize: bool,
+               expert_map: Optional[Tensor] = None, bias: Optional[Tensor] = None,
+               logits_bf16: bool = False) -> Tuple[Tensor, Tensor, Tensor]:
+    """Gate GEMM + routing in one launch: -> (topk_weights, topk_ids, fp32 logits [T, E])."""
+    _on_gpu(x, gate_w, expert_map, bias)
+    if x.dtype != gate_w.dtype or x.dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError(f"router needs x and gate weight both bf16 or both fp32, got "
+                        f"{x.dtype}/{gate_w.dtype}")
+    x, gate_w = _contig(x), _contig(gate_w)
+    T, H = x.shape
+    E = gate_w.shape[0]
+    if gate_w.shape[1] != H:
+        raise ValueError(f"gate weight {tuple(gate_w.shape)} does not match x {tuple(x.shape)}")
+    w = torch.empty(T, top_k, dtype=torch.float32, device=x.device)
+    ids = torch.empty(T, top_k, dtype=torch.int32, device=x.device)
+    logits = torch.empty(T, E, dtype=torch.float32, device=x.device)
+    m = _map_arg(expert_map, x.device)
+    b = None if bias is None else _contig(bias.to(device=x.device, dtype=torch.float32))
+    dt = TSM_BF16 if x.dtype == torch.bfloat16 else TSM_F32
+    check(lib.tsm_moe_router(ptr(x), ptr(gate_w), dt, T, H, E, top_k, int(renormalize), ptr(m),
+                             ptr(b), int(logits_bf16), ptr(logits), ptr(w), ptr(ids),
+                             stream_of(x)), "moe_router")
+    return w, ids, logits
+
+
+@moe_router.register_fake
+def _(x, gate_w, top_k, renormalize, expert_map=None, bias=None, logits_bf16=False):
+    T, E = x.shape[0], gate_w.shape[0]
+    return (x.new_empty(T, top_k, dtype=torch.float32), x.new_empty(T, top_k, dtype=torch.int32),
+            x.new_empty(T, E, dtype=torch.float32))
+
+
+# ---------------------------------------------------------------- permutation
+@torch.library.custom_op("tinyserve_amd::moe_align_block_size", mutates_args=())
+def moe_align_block_size(topk_ids: Tensor, block_m: int,
+                         num_experts: int) -> Tuple[Tensor, Tensor, Tensor]:
+    """-> (sorted_ids int32 [max_padded], expert_ids int32 [max_padded/block_m], total int32 [1])"""
+    _on_gpu(topk_ids)
+    flat = _contig(topk_ids.reshape(-1).to(torch.int32))
+    numel = flat.numel()
+    mp = int(lib.tsm_moe_max_padded(numel, num_experts, block_m))
+    if mp < 0:
+        raise ValueError("invalid num_experts / block_m")
+    dev = topk_ids.device
+    sorted_ids = torch.empty(mp, dtype=torch.int32, device=dev)
+    expert_ids = torch.empty(mp // block_m, dtype=torch.int32, device=dev)
+    total = torch.empty(1, dtype=torch.int32, device=dev)
+    nws = int(lib.tsm_moe_align_workspace_size(numel, num_experts, block_m))
+    ws = torch.empty(max(nws, 1), dtype=torch.uint8, device=dev)
+    check(lib.tsm_moe_align(ptr(flat), numel, num_experts, block_m, ptr(sorted_ids),
+                            ptr(expert_ids), ptr(total), ptr(ws), nws, stream_of(flat)),
+          "moe_align_block_size")
+    return sorted_ids, expert_ids, total
+
+
+@moe_align_block_size.register_fake
+def _(topk_ids, block_m, num_experts):
+    numel = topk_ids.numel()
+    nb = num_experts + 1
+    mp = -(-(numel + nb * (block_m - 1)) // block_m) * block_m
+    return (topk_ids.new_empty(mp, dtype=torch.int32),
+            topk_ids.new_empty(mp // block_m, dtype=torch.int32),
+            topk_ids.new_empty(1, dtype=torch.int32))
+
+
+# ---------------------------------------------------------------- activation
+@torch.library.custom_op("tinyserve_amd::silu_and_mul", mutates_args=())
+def silu_and_mul(gate: Tensor, up: Tensor) -> Tensor:
+    """bf16(bf16(silu(gate)) * up) over the last dimension (strided rows allowed)."""
+    _on_gpu(gate, up)
+    if gate.dtype != torch.bfloat16 or up.dtype != torch.bfloat16:
+        raise TypeError("silu_and_mul supports bf16 tensors")
+    if gate.shape != up.shape:
+        raise ValueError("gate and up shapes differ")
+    shape = gate.shape
+    N = shape[-1]
+    a, b = gate.reshape(-1, N), up.reshape(-1, N)
+    if a.stride(-1) != 1:
+        a = a.contiguous()
+    if b.stride(-1) != 1:
+        b = b.contiguous()
+    out = torch.empty(a.shape, dtype=gate.dtype, device=gate.device)
+    check(lib.tsm_silu_and_mul(ptr(a), a.stride(0), ptr(b), b.stride(0), ptr(out), out.stride(0),
+                               a.shape[0], N, stream_of(a)), "silu_and_mul")
+    return out.view(shape)
+
+
+@silu_and_mul.register_fake
+def _(gate, up):
+    return torch.empty_like(gate)
+
+
+# ---------------------------------------------------------------- experts
+def _check_weights(x, w13, w2):
+    if x.dtype != torch.bfloat16 or w13.dtype != torch.bfloat16 or w2.dtype != torch.bfloat16:
+        raise TypeError(f"fused_moe runs in bf16 (got x {x.dtype}, w13 {w13.dtype}, "
+                        f"w2 {w2.dtype})")
+    T, H = x.shape
+    E, two_i, H1 = w13.shape
+    I = two_i // 2
+    if H1 != H or tuple(w2.shape) != (E, H, I) or two_i != 2 * I:
+        raise ValueError(f"weight shapes w13 {tuple(w13.shape)} / w2 {tuple(w2.shape)} do not "
+                         f"match x {tuple(x.shape)}")
+    return T, H, E, I
+
+
+@torch.library.custom_op("tinyserve_amd::fused_moe", mutates_args=())
+def fused_moe(x: Tensor, w13: Tensor, w2: Tensor, topk_weights: Tensor, topk_ids: Tensor,
+              sum_topk: bool = True) -> Tensor:
+    """sum_k weight_k * expert_k(x) -> [T, H] (or the per-slot rows [T*k, H])."""
+    _on_gpu(x, w13, w2, topk_weights, topk_ids)
+    x, w13, w2 = _contig(x), _contig(w13), _contig(w2)
+    T, H, E, I = _check_weights(x, w13, w2)
+    k = topk_ids.shape[1]
+    tw = _contig(topk_weights.to(torch.float32))
+    ti = _contig(topk_ids.to(torch.int32))
+    out = torch.empty((T, H) if sum_topk else (T * k, H), dtype=x.dtype, device=x.device)
+    nws = int(lib.tsm_fused_moe_workspace_size(T, H, I, E, k))
+    ws = torch.empty(max(nws, 1), dtype=torch.uint8, device=x.device)
+    check(lib.tsm_fused_moe(ptr(x), ptr(w13), ptr(w2), ptr(tw), ptr(ti), T, H, I, E, k,
+                            int(sum_topk), ptr(out), ptr(ws), nws, stream_of(x)), "fused_moe")
+    return out
+
+
+@fused_moe.register_fake
+def _(x, w13, w2, topk_weights, topk_ids, sum_topk=True):
+    T, H = x.shape
+    k = topk_ids.shape[1]
+    return x.new_empty((T, H) if sum_topk else (T * k, H))
+
+
+@torch.library.custom_op("tinyserve_amd::moe_forward", mutates_args=())
+def moe_forward(x: Tensor, gate_w: Tensor, w13: Tensor, w2: Tensor, top_k: int,
+                renormalize: bool, expert_map: Optional[Tensor] = None,
+                bias: Optional[Tensor] = None, logits_bf16: bool = False,
+                sum_topk: bool = True) -> Tensor:
+    """Whole MoE block: fused router (gate GEMM + softmax/top-k) then the experts."""
+    _on_gpu(x, gate_w, w13, w2, expert_map, bias)
+    x, gate_w, w13, w2 = _contig(x), _contig(gate_w), _contig(w13), _contig(w2)
+    T, H, E, I = _check_weights(x, w13, w2)
+    if gate_w.dtype != torch.bfloat16 or tuple(gate_w.shape) != (E, H):
+        raise ValueError(f"gate weight must be bf16 [E, H] = [{E}, {H}]")
+    m = _map_arg(expert_map, x.device)
+    b = None if bias is None else _contig(bias.to(device=x.device, dtype=torch.float32))
+    out = torch.empty((T, H) if sum_topk else (T * top_k, H), dtype=x.dtype, device=x.device)
+    nws = int(lib.tsm_moe_forward_workspace_size(T, H, I, E, top_k))
+    ws = torch.empty(max(nws, 1), dtype=torch.uint8, device=x.device)
+    check(lib.tsm_moe_forward(ptr(x), ptr(gate_w), ptr(w13), ptr(w2), ptr(m), ptr(b), T, H, I, E,
+                              top_k, int(renormalize), int(logits_bf16), int(sum_topk), ptr(out),
+                              None, None, ptr(ws), nws, stream_of(x)), "moe_forward")
+    return out
+
+
+@moe_forward.register_fake
+def _(x, gate_w, w13, w2, top_k, renormalize, expert_map=None, bias=None, logits_bf16=False,
+      sum_topk=True):
+    T, H = x.shape
+    return x.new_empty((T, H) if sum_topk else (T * top_k, H))
