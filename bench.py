@@ -1,0 +1,299 @@
+#!/usr/bin/env python3
+"""Fused-MoE layer benchmark on one MI355X (Qwen3-30B-A3B MoE shape, bf16).
+
+A step is one MoE layer forward (fused router + align + gate_up/SwiGLU + down + k-sum) over one
+batch of T synthetic tokens, inputs and weights resident in HBM. The headline workload is the
+decode configuration T=64 (H=2048, E=128, top-8, I=768); the step cycles over 8 distinct
+random-init layer copies so expert weights are streamed from HBM, not served from the 256 MB
+Infinity Cache. The timed region replays HIP graphs of the step (one graph per layer copy).
+
+Prints ONE JSON line on stdout. Extra fields: per-stage kernel times (HIP events around each stage
+launch on the launch stream), the dominant kernel's roofline, a sweep over the decode/prefill
+token counts and the load-imbalance stress cases, and the CPU baseline (the torch-CPU restatement
+of the reference MoE path, timed on this host's cores).
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+HBM_PEAK = 8.0e12        # B/s, MI355X HBM3E
+MFMA_BF16_PEAK = 2.5e15  # flop/s, MI355X dense bf16
+H, E, K_TOP, I = 2048, 128, 8, 768
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def layer_bytes(T, n_touched):
+    """Algorithmic HBM bytes of one layer: touched expert weights + router weight + x in/out + logits."""
+    return n_touched * 3 * H * I * 2 + E * H * 2 + 2 * T * H * 2 + T * E * 2
+
+
+def layer_flops(T):
+    return 2 * T * H * E + 6 * T * K_TOP * H * I
+
+
+def stage_bytes(T, n_touched):
+    numel = T * K_TOP
+    return {
+        "router": T * H * 2 + E * H * 2 + numel * 8,
+        "align": numel * 4,
+        "gate_up": n_touched * 2 * I * H * 2 + T * H * 2 + numel * I * 2,
+        "down": n_touched * H * I * 2 + numel * I * 2 + numel * H * 2,
+        "combine": numel * H * 2 + T * H * 2,
+    }
+
+
+def stage_flops(T):
+    numel = T * K_TOP
+    return {"router": 2 * T * H * E, "gate_up": 2 * numel * H * 2 * I, "down": 2 * numel * I * H}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--tokens", type=int, default=64)
+    ap.add_argument("--layers", type=int, default=8, help="distinct layer copies cycled over")
+    ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--profile", action="store_true",
+                    help="eager stage launches only (for rocprofv3 runs); no sweep, no CPU leg")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: this build has no multi-GPU path "
+              f"(--gpus {args.gpus} requested)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    lib_path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "tinyserve_amd",
+                            "libtinyserve_moe.so")
+    if not os.path.exists(lib_path):
+        import __graft_entry__
+        __graft_entry__.build()
+    import tinyserve_amd as tsm
+    from tinyserve_amd._lib import check, lib, ptr
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    g = torch.Generator(device=dev).manual_seed(0)
+    L = args.layers
+    log(f"allocating {L} layer copies")
+    layers = []
+    for _ in range(L):
+        gw = (torch.randn(E, H, generator=g, device=dev) * 0.02).bfloat16()
+        w13 = (torch.randn(E, 2 * I, H, generator=g, device=dev) * 0.02).bfloat16()
+        w2 = (torch.randn(E, H, I, generator=g, device=dev) * 0.02).bfloat16()
+        layers.append((gw, w13, w2))
+
+    def inputs(T, seed):
+        gg = torch.Generator(device=dev).manual_seed(seed)
+        return [torch.randn(T, H, generator=gg, device=dev).bfloat16() for _ in range(L)]
+
+    def time_layer(T, steps, warmup, bias=None):
+        """HIP-graph replays of the whole layer, cycling the layer copies. Returns (ms/step,
+        mean touched experts)."""
+        xs = inputs(T, 1000 + T)
+        touched = []
+        for i in range(L):
+            _, ids, _ = tsm.moe_router(xs[i], layers[i][0], K_TOP, True, None, bias)
+            touched.append(int(torch.unique(ids).numel()))
+        graphs = []
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for i in range(L):
+                tsm.moe_forward(xs[i], *layers[i], K_TOP, True, None, bias)
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        for i in range(L):
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr):
+                tsm.moe_forward(xs[i], *layers[i], K_TOP, True, None, bias)
+            graphs.append(gr)
+        for j in range(warmup):
+            graphs[j % L].replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for j in range(steps):
+            graphs[j % L].replay()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / steps
+        del graphs
+        return ms, sum(touched) / len(touched)
+
+    def time_stages(T, steps, warmup):
+        """Eager launches of each stage through the C ABI with HIP events between stages on the
+        launch stream. Returns mean ms per stage launch."""
+        xs = inputs(T, 1000 + T)
+        numel = T * K_TOP
+        bm = int(lib.tsm_moe_block_m(T, H, I, E, K_TOP))
+        mp = int(lib.tsm_moe_max_padded(numel, E, bm))
+        w = torch.empty(T, K_TOP, dtype=torch.float32, device=dev)
+        ids = torch.empty(T, K_TOP, dtype=torch.int32, device=dev)
+        sorted_ids = torch.empty(mp, dtype=torch.int32, device=dev)
+        eids = torch.empty(mp // bm, dtype=torch.int32, device=dev)
+        total = torch.empty(1, dtype=torch.int32, device=dev)
+        nws = int(lib.tsm_moe_align_workspace_size(numel, E, bm))
+        aws = torch.empty(max(nws, 1), dtype=torch.uint8, device=dev)
+        act = torch.empty(mp, I, dtype=torch.bfloat16, device=dev)
+        rows = torch.empty(numel, H, dtype=torch.bfloat16, device=dev)
+        out = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
+        stream = torch.cuda.current_stream()
+        sp = stream.cuda_stream
+        names = ["router", "align", "gate_up", "down", "combine"]
+        acc = {n: 0.0 for n in names}
+
+        def one(i, evs):
+            gw, w13, w2 = layers[i % L]
+            x = xs[i % L]
+            if evs: evs[0].record(stream)
+            check(lib.tsm_moe_router(ptr(x), ptr(gw), 1, T, H, E, K_TOP, 1, None, None, 0, None,
+                                     ptr(w), ptr(ids), sp), "router")
+            if evs: evs[1].record(stream)
+            check(lib.tsm_moe_align(ptr(ids), numel, E, bm, ptr(sorted_ids), ptr(eids),
+                                    ptr(total), ptr(aws), nws, sp), "align")
+            if evs: evs[2].record(stream)
+            check(lib.tsm_moe_gemm_gate_up(ptr(x), ptr(w13), ptr(sorted_ids), ptr(eids),
+                                           ptr(total), numel, K_TOP, H, I, E, bm, ptr(act), sp),
+                  "gate_up")
+            if evs: evs[3].record(stream)
+            check(lib.tsm_moe_gemm_down(ptr(act), ptr(w2), ptr(w), ptr(sorted_ids), ptr(eids),
+                                        ptr(total), numel, H, I, E, bm, ptr(rows), sp), "down")
+            if evs: evs[4].record(stream)
+            check(lib.tsm_moe_combine(ptr(rows), T, H, K_TOP, ptr(out), sp), "combine")
+            if evs: evs[5].record(stream)
+
+        for j in range(warmup):
+            one(j, None)
+        torch.cuda.synchronize()
+        all_evs = []
+        for j in range(steps):
+            evs = [torch.cuda.Event(enable_timing=True) for _ in range(6)]
+            one(j, evs)
+            all_evs.append(evs)
+        torch.cuda.synchronize()
+        for evs in all_evs:
+            for k, n in enumerate(names):
+                acc[n] += evs[k].elapsed_time(evs[k + 1])
+        return {n: acc[n] / steps for n in names}, bm
+
+    T = args.tokens
+    log(f"stage timing T={T}")
+    stages_ms, bm = time_stages(T, args.steps, args.warmup)
+    if args.profile:
+        print(json.dumps({"profile_run": True, "tokens": T, "stages_ms": stages_ms}), flush=True)
+        return
+
+    log(f"layer timing T={T}")
+    ms, n_touched = time_layer(T, args.steps, args.warmup)
+    B = layer_bytes(T, n_touched)
+    F = layer_flops(T)
+    t = ms * 1e-3
+    sb = stage_bytes(T, n_touched)
+    sf = stage_flops(T)
+    dom = "gate_up"
+    dom_t = stages_ms[dom] * 1e-3
+    roofline = {
+        "kernel": "moe_gemm_kernel<gate_up> (gate_up GEMM + SwiGLU epilogue)",
+        "bound": "hbm",
+        "achieved": sb[dom] / dom_t / 1e9,
+        "peak": HBM_PEAK / 1e9,
+        "unit": "GB/s",
+        "frac": sb[dom] / dom_t / HBM_PEAK,
+        "traffic": None,
+        "algorithmic_bytes_per_launch": sb[dom],
+        "avg_launch_us": stages_ms[dom] * 1e3,
+        "layer_frac_of_roofline": max(B / HBM_PEAK, F / MFMA_BF16_PEAK) / t,
+    }
+    res = {
+        "metric": "fused-MoE layer HBM GB/s, Qwen3-30B-A3B decode T=64 (bf16)",
+        "value": B / t / 1e9,
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (x~N(0,1), random-init weights std 0.02, seed 0)",
+        "config": {"workload": f"Qwen3-30B-A3B MoE layer decode, T={T} tokens", "tokens": T,
+                   "hidden": H, "experts": E, "top_k": K_TOP, "moe_intermediate": I,
+                   "norm_topk_prob": True, "layer_copies": L, "block_m": bm,
+                   "n_touched": n_touched},
+        "us_per_layer": ms * 1e3,
+        "tokens_per_s": T / t,
+        "tflops": F / t / 1e12,
+        "stages_us": {k: v * 1e3 for k, v in stages_ms.items()},
+        "stages_gbps": {k: sb[k] / (stages_ms[k] * 1e-3) / 1e9 for k in sb},
+        "roofline": roofline,
+    }
+
+    if not args.no_sweep:
+        sweep = []
+        for Ts in (1, 8, 64, 256, 512, 2048, 8192):
+            steps = 30 if Ts <= 2048 else 12
+            mss, nt = time_layer(Ts, steps, 5)
+            Bs, Fs = layer_bytes(Ts, nt), layer_flops(Ts)
+            ts = mss * 1e-3
+            sweep.append({"tokens": Ts, "us": mss * 1e3, "GBps": Bs / ts / 1e9,
+                          "TFLOPS": Fs / ts / 1e12, "frac_hbm": Bs / ts / HBM_PEAK,
+                          "frac_mfma": Fs / ts / MFMA_BF16_PEAK,
+                          "frac_roofline": max(Bs / HBM_PEAK, Fs / MFMA_BF16_PEAK) / ts,
+                          "n_touched": nt})
+            log(json.dumps(sweep[-1]))
+        for kind in ("zipf", "half_empty"):
+            gen = torch.Generator().manual_seed(1)
+            if kind == "zipf":
+                p = 1.0 / torch.arange(1, E + 1, dtype=torch.float64) ** 1.2
+                p = p[torch.randperm(E, generator=gen)]
+                bias = torch.log(p / p.sum()).float().to(dev)
+            else:
+                bias = torch.zeros(E, device=dev)
+                bias[E // 2:] = float("-inf")
+            mss, nt = time_layer(2048, 30, 5, bias)
+            Bs, Fs = layer_bytes(2048, nt), layer_flops(2048)
+            ts = mss * 1e-3
+            sweep.append({"tokens": 2048, "stress": kind, "us": mss * 1e3, "GBps": Bs / ts / 1e9,
+                          "TFLOPS": Fs / ts / 1e12,
+                          "frac_roofline": max(Bs / HBM_PEAK, Fs / MFMA_BF16_PEAK) / ts,
+                          "n_touched": nt})
+            log(json.dumps(sweep[-1]))
+        res["sweep"] = sweep
+
+    if not args.no_cpu_baseline:
+        from oracle.moe_oracle import moe_reference, route_torch
+        threads = torch.get_num_threads()
+        gw, w13, w2 = (t_.cpu() for t_ in layers[0])
+        x = inputs(T, 1000 + T)[0].cpu()
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            logits = (x @ gw.t()).float()
+            wc, idc = route_torch(logits, K_TOP, True)
+            moe_reference(x, w13, w2, wc, idc)
+            reps += 1
+            el = time.perf_counter() - t0
+            if (el >= args.cpu_seconds and reps >= 3) or el > 4 * args.cpu_seconds:
+                break
+        tc = el / reps
+        nt_c = int(torch.unique(idc).numel())
+        res["cpu_baseline"] = {"value": layer_bytes(T, nt_c) / tc / 1e9, "unit": "GB/s",
+                               "cores": threads, "kind": "port",
+                               "sample": f"{reps} layer forwards at T={T} (torch-CPU bf16 "
+                                         f"restatement of serve.py router + moe_reference), "
+                                         f"{el:.1f} s total, {tc * 1e3:.1f} ms/layer"}
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

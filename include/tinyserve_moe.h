@@ -118,6 +118,29 @@ int tsm_fused_moe(const void* x, const void* w13, const void* w2, const float* t
                   int sum_topk, void* out, void* ws, size_t ws_bytes, hipStream_t stream);
 
 /*
+ * The stages of tsm_fused_moe, for callers that schedule them separately (and for per-kernel
+ * timing). Each is one launch of the corresponding stage of _moe_gemm / _fused_moe_kernel
+ * (tinykernels.py:1746-1765, 1589-1744) on the outputs of tsm_moe_align for the same block_m
+ * (supported: 16, 64):
+ *   gate_up: act[max_padded, I] (expert-sorted rows) = bf16(bf16(silu(bf16(x W1^T))) *
+ *            bf16(x W3^T)) with x gathered as x[sorted_ids[r] / top_k]; rows of remote tiles
+ *            are not written.
+ *   down:    rows[a, :] = bf16((act[r] W2^T) * topk_w[a]) for a = sorted_ids[r] < numel; zeros
+ *            for remote assignments. top_k is 1 for this GEMM (act rows are assignments).
+ *   combine: out[t, :] = bf16(sum_{s<k} rows[t*k + s, :]), fp32 accumulation in slot order
+ *            (tinykernels.py:1796).
+ */
+int tsm_moe_gemm_gate_up(const void* x, const void* w13, const int32_t* sorted_ids,
+                         const int32_t* expert_ids, const int32_t* total, int64_t numel,
+                         int top_k, int H, int I, int E, int block_m, void* act,
+                         hipStream_t stream);
+int tsm_moe_gemm_down(const void* act, const void* w2, const float* topk_w,
+                      const int32_t* sorted_ids, const int32_t* expert_ids, const int32_t* total,
+                      int64_t numel, int H, int I, int E, int block_m, void* rows,
+                      hipStream_t stream);
+int tsm_moe_combine(const void* rows, int64_t T, int H, int top_k, void* out, hipStream_t stream);
+
+/*
  * Whole SparseMoE.forward on one GPU (serve.py:1076-1087 at TP=1): fused router then fused_moe.
  * Router options as in tsm_moe_router; topk_w/topk_ids ([T, k]) may be null when the caller does
  * not need them (they then live in the workspace).

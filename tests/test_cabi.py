@@ -1,0 +1,71 @@
+"""CPU tests of the C ABI: the library loads, exports every symbol declared in
+include/tinyserve_moe.h, and its size/validation entry points behave (no kernel launches)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "tinyserve_moe.h")
+LIB = os.path.join(ROOT, "tinyserve_amd", "libtinyserve_moe.so")
+
+
+def declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(tsm_\w+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(LIB):
+        pytest.fail("libtinyserve_moe.so not built (run __graft_entry__.build())")
+    import torch  # noqa: F401  (same load order as the package)
+    return ctypes.CDLL(LIB)
+
+
+def test_every_declared_symbol_is_exported(lib):
+    names = declared()
+    assert len(names) >= 15
+    for n in names:
+        assert hasattr(lib, n), n
+
+
+def test_package_signatures_cover_header():
+    import tinyserve_amd._lib as L
+    src = open(L.__file__).read()
+    for n in declared():
+        assert f'"{n}"' in src, n
+
+
+def test_sizes(lib):
+    lib.tsm_moe_max_padded.restype = ctypes.c_int64
+    lib.tsm_moe_max_padded.argtypes = [ctypes.c_int64, ctypes.c_int, ctypes.c_int]
+    assert lib.tsm_moe_max_padded(512, 128, 16) == 2448       # T=64 decode
+    assert lib.tsm_moe_max_padded(65536, 128, 64) == 73664    # T=8192 prefill
+    assert lib.tsm_moe_max_padded(4, 3, 4) == 16              # docstring example
+    lib.tsm_fused_moe_workspace_size.restype = ctypes.c_size_t
+    lib.tsm_fused_moe_workspace_size.argtypes = [ctypes.c_int64] + [ctypes.c_int] * 4
+    assert lib.tsm_fused_moe_workspace_size(64, 2048, 768, 128, 8) > 2448 * 768 * 2
+    lib.tsm_abi_version.restype = ctypes.c_int
+    assert lib.tsm_abi_version() == 1
+
+
+def test_invalid_arguments_return_codes(lib):
+    """Validation happens before any HIP call, so these run without a GPU."""
+    P, I64, I32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
+    lib.tsm_last_error.restype = ctypes.c_char_p
+    f = lib.tsm_moe_route
+    f.argtypes = [P, I32, I64, I32, I64, I32, I32, P, P, P, P]
+    assert f(None, 0, 4, 128, 128, 0, 1, None, None, None, None) == -1          # top_k = 0
+    assert b"top_k" in lib.tsm_last_error()
+    assert f(None, 0, 4, 1000, 1000, 8, 1, None, None, None, None) == -2        # E > 512
+    assert f(None, 7, 4, 128, 128, 8, 1, None, P(16), P(16), P(16)) == -1       # null logits
+    g = lib.tsm_fused_moe
+    g.argtypes = [P, P, P, P, P, I64, I32, I32, I32, I32, I32, P, P, ctypes.c_size_t, P]
+    assert g(P(256), P(256), P(256), P(256), P(256), 4, 100, 768, 128, 8, 1, P(256), P(256),
+             1 << 30, None) == -2                                                # H % 128
+    assert g(P(256), P(256), P(256), P(256), P(256), 4, 2048, 768, 128, 8, 1, P(256), P(256),
+             16, None) == -4                                                     # workspace
+    assert b"workspace" in lib.tsm_last_error()
+    assert g(None, None, None, None, None, 0, 2048, 768, 128, 8, 1, None, None, 0, None) == 0

@@ -268,15 +268,6 @@ Plan plan_for(int64_t T, int E, int top_k) {
     return Plan{64, kPrefill};
 }
 
-template <int BM, int BN, int WM, int WN>
-hipError_t launch_pair(const GemmArgs& g1, const GemmArgs& g2, hipStream_t stream) {
-    hipLaunchKernelGGL((moe_gemm_kernel<BM, BN, WM, WN, true>), dim3(g1.m_tiles * g1.n_tiles),
-                       dim3(256), 0, stream, g1);
-    hipLaunchKernelGGL((moe_gemm_kernel<BM, BN, WM, WN, false>), dim3(g2.m_tiles * g2.n_tiles),
-                       dim3(256), 0, stream, g2);
-    return hipGetLastError();
-}
-
 constexpr int kBN = 128;  // B rows per workgroup tile (both variants)
 
 struct Layout {
@@ -318,13 +309,67 @@ int check_moe_shapes(int64_t T, int H, int I, int E, int top_k) {
     return check_align_args(T * top_k, E, 64);
 }
 
+GemmArgs gemm_args(const bf16_t* A, const bf16_t* B, bf16_t* C, const float* topk_w,
+                   const int32_t* sorted, const int32_t* eids, const int32_t* total,
+                   int64_t numel, int top_k, int N, int K, int E, int block_m, int n_tiles) {
+    GemmArgs g{};
+    g.A = A;
+    g.B = B;
+    g.C = C;
+    g.topk_w = topk_w;
+    g.sorted_ids = sorted;
+    g.expert_ids = eids;
+    g.total = total;
+    g.numel = numel;
+    g.top_k = top_k;
+    g.N = N;
+    g.K = K;
+    g.m_tiles = (int)(max_padded_rows(numel, E, block_m) / block_m);
+    g.n_tiles = n_tiles;
+    return g;
+}
+
+bool block_m_supported(int block_m) { return block_m == 16 || block_m == 64; }
+
+// gate_up GEMM + SwiGLU: act[max_padded, I] from x[T, H] and w13[E, 2I, H].
+void launch_gate_up(const bf16_t* x, const bf16_t* w13, const int32_t* sorted,
+                    const int32_t* eids, const int32_t* total, int64_t numel, int top_k, int H,
+                    int I, int E, int block_m, bf16_t* act, hipStream_t stream) {
+    GemmArgs g = gemm_args(x, w13, act, nullptr, sorted, eids, total, numel, top_k, I, H, E,
+                           block_m, I / (kBN / 2));
+    const dim3 grid(g.m_tiles * g.n_tiles);
+    if (block_m == 16)
+        hipLaunchKernelGGL((moe_gemm_kernel<16, kBN, 1, 4, true>), grid, dim3(256), 0, stream, g);
+    else
+        hipLaunchKernelGGL((moe_gemm_kernel<64, kBN, 2, 2, true>), grid, dim3(256), 0, stream, g);
+}
+
+// down GEMM * routing weight: rows[numel, H] from act[max_padded, I] and w2[E, H, I].
+void launch_down(const bf16_t* act, const bf16_t* w2, const float* topk_w, const int32_t* sorted,
+                 const int32_t* eids, const int32_t* total, int64_t numel, int H, int I, int E,
+                 int block_m, bf16_t* rows, hipStream_t stream) {
+    GemmArgs g = gemm_args(act, w2, rows, topk_w, sorted, eids, total, numel, 1, H, I, E,
+                           block_m, H / kBN);
+    const dim3 grid(g.m_tiles * g.n_tiles);
+    if (block_m == 16)
+        hipLaunchKernelGGL((moe_gemm_kernel<16, kBN, 1, 4, false>), grid, dim3(256), 0, stream, g);
+    else
+        hipLaunchKernelGGL((moe_gemm_kernel<64, kBN, 2, 2, false>), grid, dim3(256), 0, stream, g);
+}
+
+void launch_combine(const bf16_t* rows, int64_t T, int H, int top_k, bf16_t* out,
+                    hipStream_t stream) {
+    const int64_t threads = T * (H / 8);
+    hipLaunchKernelGGL(combine_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
+                       stream, rows, out, T, H, top_k);
+}
+
 // Everything after routing: align, gate_up + SwiGLU, down * weight, k-sum.
 int run_experts(const void* x, const void* w13, const void* w2, const float* topk_w,
                 const int32_t* topk_ids, int64_t T, int H, int I, int E, int top_k, int sum_topk,
                 void* out, char* ws, const Layout& L, hipStream_t stream) {
     const Plan pl = plan_for(T, E, top_k);
     const int64_t numel = T * top_k;
-    const int64_t mp = max_padded_rows(numel, E, pl.block_m);
     int32_t* sorted = reinterpret_cast<int32_t*>(ws + L.sorted);
     int32_t* eids = reinterpret_cast<int32_t*>(ws + L.expert_ids);
     int32_t* total = reinterpret_cast<int32_t*>(ws + L.total);
@@ -332,38 +377,11 @@ int run_experts(const void* x, const void* w13, const void* w2, const float* top
     bf16_t* rows = sum_topk ? reinterpret_cast<bf16_t*>(ws + L.rows) : (bf16_t*)out;
 
     (void)launch_align(topk_ids, numel, E, pl.block_m, sorted, eids, total, ws + L.hist, stream);
-
-    GemmArgs g1{};
-    g1.A = (const bf16_t*)x;
-    g1.B = (const bf16_t*)w13;
-    g1.C = act;
-    g1.topk_w = topk_w;
-    g1.sorted_ids = sorted;
-    g1.expert_ids = eids;
-    g1.total = total;
-    g1.numel = numel;
-    g1.top_k = top_k;
-    g1.N = I;
-    g1.K = H;
-    g1.m_tiles = (int)(mp / pl.block_m);
-    g1.n_tiles = I / (kBN / 2);
-    GemmArgs g2 = g1;
-    g2.A = act;
-    g2.B = (const bf16_t*)w2;
-    g2.C = rows;
-    g2.N = H;
-    g2.K = I;
-    g2.n_tiles = H / kBN;
-    if (pl.v == kDecode)
-        (void)launch_pair<16, kBN, 1, 4>(g1, g2, stream);
-    else
-        (void)launch_pair<64, kBN, 2, 2>(g1, g2, stream);
-
-    if (sum_topk) {
-        const int64_t threads = T * (H / 8);
-        hipLaunchKernelGGL(combine_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
-                           stream, rows, (bf16_t*)out, T, H, top_k);
-    }
+    launch_gate_up((const bf16_t*)x, (const bf16_t*)w13, sorted, eids, total, numel, top_k, H, I,
+                   E, pl.block_m, act, stream);
+    launch_down(act, (const bf16_t*)w2, topk_w, sorted, eids, total, numel, H, I, E, pl.block_m,
+                rows, stream);
+    if (sum_topk) launch_combine(rows, T, H, top_k, (bf16_t*)out, stream);
     return check_launch("fused_moe kernels");
 }
 
@@ -445,4 +463,48 @@ extern "C" int tsm_moe_forward(const void* x, const void* gate_w, const void* w1
                         logits_bf16, nullptr, tw, ti, stream);
     if (rc) return rc;
     return run_experts(x, w13, w2, tw, ti, T, H, I, E, top_k, sum_topk, out, w, L, stream);
+}
+
+extern "C" int tsm_moe_gemm_gate_up(const void* x, const void* w13, const int32_t* sorted_ids,
+                                    const int32_t* expert_ids, const int32_t* total,
+                                    int64_t numel, int top_k, int H, int I, int E, int block_m,
+                                    void* act, hipStream_t stream) {
+    clear_error();
+    int rc = check_moe_shapes(numel / (top_k > 0 ? top_k : 1), H, I, E, top_k);
+    if (rc) return rc;
+    TSM_REQUIRE(block_m_supported(block_m), TSM_E_SHAPE, "block_m %d has no kernel (16 or 64)",
+                block_m);
+    if (numel == 0) return TSM_OK;
+    TSM_REQUIRE(x && w13 && sorted_ids && expert_ids && total && act, TSM_E_ARG,
+                "null pointer argument");
+    launch_gate_up((const bf16_t*)x, (const bf16_t*)w13, sorted_ids, expert_ids, total, numel,
+                   top_k, H, I, E, block_m, (bf16_t*)act, stream);
+    return check_launch("gate_up GEMM");
+}
+
+extern "C" int tsm_moe_gemm_down(const void* act, const void* w2, const float* topk_w,
+                                 const int32_t* sorted_ids, const int32_t* expert_ids,
+                                 const int32_t* total, int64_t numel, int H, int I, int E,
+                                 int block_m, void* rows, hipStream_t stream) {
+    clear_error();
+    int rc = check_moe_shapes(numel, H, I, E, 1);
+    if (rc) return rc;
+    TSM_REQUIRE(block_m_supported(block_m), TSM_E_SHAPE, "block_m %d has no kernel (16 or 64)",
+                block_m);
+    if (numel == 0) return TSM_OK;
+    TSM_REQUIRE(act && w2 && topk_w && sorted_ids && expert_ids && total && rows, TSM_E_ARG,
+                "null pointer argument");
+    launch_down((const bf16_t*)act, (const bf16_t*)w2, topk_w, sorted_ids, expert_ids, total,
+                numel, H, I, E, block_m, (bf16_t*)rows, stream);
+    return check_launch("down GEMM");
+}
+
+extern "C" int tsm_moe_combine(const void* rows, int64_t T, int H, int top_k, void* out,
+                               hipStream_t stream) {
+    clear_error();
+    TSM_REQUIRE(T >= 0 && H > 0 && H % 8 == 0 && top_k >= 1, TSM_E_ARG, "bad combine sizes");
+    if (T == 0) return TSM_OK;
+    TSM_REQUIRE(rows && out, TSM_E_ARG, "null pointer argument");
+    launch_combine((const bf16_t*)rows, T, H, top_k, (bf16_t*)out, stream);
+    return check_launch("combine");
 }
