@@ -42,6 +42,9 @@ enum {
 /* dtype codes */
 enum { TSM_F32 = 0, TSM_BF16 = 1 };
 
+/* expert weight layouts */
+enum { TSM_LAYOUT_REFERENCE = 0, TSM_LAYOUT_PACKED = 1 };
+
 /* Description of the last error on the calling thread ("" if none). */
 const char* tsm_last_error(void);
 
@@ -129,15 +132,17 @@ int tsm_fused_moe(const void* x, const void* w13, const void* w2, const float* t
  *            for remote assignments. top_k is 1 for this GEMM (act rows are assignments).
  *   combine: out[t, :] = bf16(sum_{s<k} rows[t*k + s, :]), fp32 accumulation in slot order
  *            (tinykernels.py:1796).
+ * weight_layout: TSM_LAYOUT_REFERENCE (w13/w2 as above) or TSM_LAYOUT_PACKED
+ * (tsm_moe_pack_weights output).
  */
 int tsm_moe_gemm_gate_up(const void* x, const void* w13, const int32_t* sorted_ids,
                          const int32_t* expert_ids, const int32_t* total, int64_t numel,
-                         int top_k, int H, int I, int E, int block_m, void* act,
-                         hipStream_t stream);
+                         int top_k, int H, int I, int E, int block_m, int weight_layout,
+                         void* act, hipStream_t stream);
 int tsm_moe_gemm_down(const void* act, const void* w2, const float* topk_w,
                       const int32_t* sorted_ids, const int32_t* expert_ids, const int32_t* total,
-                      int64_t numel, int H, int I, int E, int block_m, void* rows,
-                      hipStream_t stream);
+                      int64_t numel, int H, int I, int E, int block_m, int weight_layout,
+                      void* rows, hipStream_t stream);
 int tsm_moe_combine(const void* rows, int64_t T, int H, int top_k, void* out, hipStream_t stream);
 
 /*
@@ -151,6 +156,27 @@ int tsm_moe_forward(const void* x, const void* gate_w, const void* w13, const vo
                     int top_k, int renorm, int logits_bf16, int sum_topk, void* out,
                     float* topk_w, int32_t* topk_ids, void* ws, size_t ws_bytes,
                     hipStream_t stream);
+
+/*
+ * MFMA-tiled ("packed") expert weights. No counterpart in the reference, which streams w13/w2 in
+ * their checkpoint layout (tinykernels.py:1707-1738); this is a one-time reordering (same size)
+ * after which every 16x16x32 MFMA operand of a 16-row block is 1 KiB of contiguous memory:
+ *   packed[e][blk][s][lane][i] = W[e][16*src(blk) + lane%16][32*s + 8*(lane/16) + i]
+ * with src(blk) = blk for w2 ([E, H, I]: N = H, K = I, interleave_halves = 0) and, for w13
+ * ([E, 2I, H]: N = 2I, K = H, interleave_halves = 1), src(2j) = j, src(2j+1) = I/16 + j (gate
+ * block j next to its up block). Requires N % 16 == 0 (N % 32 with interleaving), K % 32 == 0.
+ * The *_packed entry points are tsm_fused_moe / tsm_moe_forward on packed weights.
+ */
+int tsm_moe_pack_weights(const void* w, int64_t E, int N, int K, int interleave_halves, void* out,
+                         hipStream_t stream);
+int tsm_fused_moe_packed(const void* x, const void* w13p, const void* w2p, const float* topk_w,
+                         const int32_t* topk_ids, int64_t T, int H, int I, int E, int top_k,
+                         int sum_topk, void* out, void* ws, size_t ws_bytes, hipStream_t stream);
+int tsm_moe_forward_packed(const void* x, const void* gate_w, const void* w13p, const void* w2p,
+                           const int64_t* expert_map, const float* bias, int64_t T, int H, int I,
+                           int E, int top_k, int renorm, int logits_bf16, int sum_topk, void* out,
+                           float* topk_w, int32_t* topk_ids, void* ws, size_t ws_bytes,
+                           hipStream_t stream);
 
 #ifdef __cplusplus
 }

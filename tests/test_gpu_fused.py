@@ -151,8 +151,10 @@ def test_sparse_moe_module(dev, tsm, qwen_layer):
     cfg = SimpleNamespace(num_experts=128, hidden_size=2048, moe_intermediate_size=768,
                           num_experts_per_tok=8, norm_topk_prob=True)
     x = xrand(16, 2048, dev, 8)
-    for router in ("fused", "linear"):
-        m = tsm.SparseMoE(cfg, router=router).to(device=dev, dtype=torch.bfloat16)
+    for router, packed in (("fused", True), ("linear", True), ("fused", False),
+                           ("linear", False)):
+        m = tsm.SparseMoE(cfg, router=router, packed=packed).to(device=dev,
+                                                                dtype=torch.bfloat16)
         with torch.no_grad():
             m.gate.weight.copy_(gw)
             m.w13.copy_(w13)
@@ -163,7 +165,7 @@ def test_sparse_moe_module(dev, tsm, qwen_layer):
             else:
                 w, ids = tsm.moe_route(m.gate(x), 8, True, m.expert_map)
         ref = moe_reference(x.cpu(), w13c, w2c, w.cpu(), ids.cpu().long())
-        assert_close(out, ref, f"SparseMoE {router}")
+        assert_close(out, ref, f"SparseMoE {router} packed={packed}")
 
 
 def test_moe_forward_bf16_logits_mode(dev, tsm, qwen_layer):
@@ -211,3 +213,60 @@ def test_silu_and_mul(dev, tsm):
     diff = (out.float() - ref.float()).abs()
     ulp = ref.float().abs().clamp_min(1e-30) * 2.0 ** -6  # two bf16 ulps
     assert bool((diff <= ulp + 1e-30).all())
+
+
+def test_pack_layout_matches_definition(dev, tsm):
+    """packed[e][blk][s][lane][i] = W[e][16*src(blk) + lane%16][32*s + 8*(lane//16) + i]."""
+    E, I, H = 3, 64, 256
+    w13 = torch.randn(E, 2 * I, H, device=dev).bfloat16()
+    w2 = torch.randn(E, H, I, device=dev).bfloat16()
+    p13, p2 = tsm.pack_moe_weights(w13, w2)
+
+    def ref(W, interleave):
+        E_, N, K = W.shape
+        blocks = W.view(E_, N // 16, 16, K // 32, 4, 8)            # e, blk, r, s, q, i
+        if interleave:
+            nb = N // 16
+            order = [j // 2 if j % 2 == 0 else nb // 2 + j // 2 for j in range(nb)]
+            blocks = blocks[:, order]
+        return blocks.permute(0, 1, 3, 4, 2, 5).reshape(E_, N, K)  # e, blk, s, lane=(q,r), i
+
+    assert torch.equal(p13.cpu(), ref(w13.cpu(), True))
+    assert torch.equal(p2.cpu(), ref(w2.cpu(), False))
+
+
+@pytest.mark.parametrize("T", [1, 8, 64, 256, 2048])
+def test_packed_path_bitexact_with_reference_layout(dev, tsm, qwen_layer, T):
+    """The packed kernels consume the same k order per lane as the reference-layout kernels, so
+    outputs are identical bit for bit; and both match the oracle."""
+    (gw, w13, w2), (_, w13c, w2c) = qwen_layer
+    p13, p2 = tsm.pack_moe_weights(w13, w2)
+    x = xrand(T, 2048, dev, 40 + T)
+    a = tsm.moe_forward(x, gw, w13, w2, 8, True)
+    b = tsm.moe_forward_packed(x, gw, p13, p2, 8, True)
+    assert torch.equal(a, b)
+    w, ids, _ = tsm.moe_router(x, gw, 8, True)
+    rows = tsm.fused_moe_packed(x, p13, p2, w, ids, sum_topk=False)
+    assert torch.equal(rows, tsm.fused_moe(x, w13, w2, w, ids, sum_topk=False))
+    if T <= 256:
+        ref = moe_reference(x.cpu(), w13c, w2c, w.cpu(), ids.cpu().long())
+        assert_close(b, ref, f"packed T={T}")
+
+
+def test_packed_expert_parallel_and_tiny(dev, tsm, qwen_layer):
+    (gw, w13, w2), (_, w13c, w2c) = qwen_layer
+    p13, p2 = tsm.pack_moe_weights(w13, w2)
+    emap = torch.arange(128, dtype=torch.int64, device=dev)
+    emap[::2] = -1
+    x = xrand(50, 2048, dev, 77)
+    w, ids, _ = tsm.moe_router(x, gw, 8, True, emap)
+    out = tsm.fused_moe_packed(x, p13, p2, w, ids)
+    ref = moe_reference(x.cpu(), w13c, w2c, w.cpu(), ids.cpu().long())
+    assert_close(out, ref, "packed EP")
+    from oracle.moe_oracle import make_layer
+    x, gw, w13, w2 = make_layer(37, 256, 8, 512, torch.bfloat16, seed=0, device=dev)
+    p13, p2 = tsm.pack_moe_weights(w13, w2)
+    w, ids, _ = tsm.moe_router(x, gw, 2, True)
+    out = tsm.fused_moe_packed(x, p13, p2, w, ids)
+    ref = moe_reference(x.cpu(), w13.cpu(), w2.cpu(), w.cpu(), ids.cpu().long())
+    assert_close(out, ref, "packed tiny")

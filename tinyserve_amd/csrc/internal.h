@@ -12,5 +12,28 @@ hipError_t launch_align(const int32_t* ids, int64_t numel, int E, int block_m,
                         int32_t* sorted_ids, int32_t* expert_ids, int32_t* total, void* ws,
                         hipStream_t stream);
 
+// Arguments of the grouped expert GEMM kernels (rows are expert-sorted, padded per expert to the
+// tile height, as produced by the align kernels).
+struct GemmArgs {
+    const uint16_t* A;          // gate_up: x [T, K]; down: act [max_padded, K]
+    const uint16_t* B;          // gate_up: w13 [E, 2N, K]; down: w2 [E, N, K]
+    uint16_t* C;                // gate_up: act [max_padded, N]; down: rows [numel, N]
+    const float* topk_w;        // down only: [numel]
+    const int32_t* sorted_ids;  // [max_padded]
+    const int32_t* expert_ids;  // [max_padded / tile height]
+    const int32_t* total;       // [1]
+    int64_t numel;
+    int top_k;
+    int N;                      // output columns (gate_up: I; down: H)
+    int K;                      // reduction length (gate_up: H; down: I)
+    int m_tiles;
+    int n_tiles;
+};
+
+// Weight-streaming kernels for 16-row tiles; false if the shape has no instantiation. `packed`
+// selects the MFMA-tiled weight layout (see moe_pack.hip) instead of the reference layout.
+bool launch_stream_gate_up(GemmArgs g, bool packed, hipStream_t stream);
+bool launch_stream_down(GemmArgs g, bool packed, hipStream_t stream);
+
 inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 }  // namespace tsm

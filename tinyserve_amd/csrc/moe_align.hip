@@ -145,31 +145,23 @@ __global__ __launch_bounds__(kThreads) void align_place_kernel(
         __syncthreads();
     }
 
-    // 4. padding rows (disjoint from the rows any slice places) and the unused tail
+    // 4. padding rows and tile -> expert entries, one bucket per thread (rows [start+cnt, end)
+    //    of a bucket are padding; its tiles are [start/bm, end/bm)), then the unused tail.
     const int pad_value = (int)numel;
-    for (int b = slice; b < NB; b += num_slices) {
-        const int start = pend[b] - (cnt[b] + block_m - 1) / block_m * block_m;
-        for (int r = start + cnt[b] + tid; r < pend[b]; r += kThreads) sorted_ids[r] = pad_value;
+    for (int b = slice + num_slices * tid; b < NB; b += num_slices * kThreads) {
+        const int end = pend[b];
+        const int start = end - (cnt[b] + block_m - 1) / block_m * block_m;
+        for (int r = start + cnt[b]; r < end; ++r) sorted_ids[r] = pad_value;
+        const int eid = b < E ? b : -1;
+        for (int tl = start / block_m; tl < end / block_m; ++tl) expert_ids[tl] = eid;
     }
     const int used = pend[NB - 1];
-    const int64_t tail = max_padded - used;
-    for (int64_t r = used + (int64_t)slice * kThreads + tid; r < max_padded;
-         r += (int64_t)num_slices * kThreads)
+    const int64_t stride = (int64_t)num_slices * kThreads;
+    for (int64_t r = used + (int64_t)slice * kThreads + tid; r < max_padded; r += stride)
         sorted_ids[r] = pad_value;
-    (void)tail;
-
-    // 5. tile -> expert table and the used row count
     const int64_t tiles = max_padded / block_m;
-    for (int64_t tl = (int64_t)slice * kThreads + tid; tl < tiles;
-         tl += (int64_t)num_slices * kThreads) {
-        const int64_t row = tl * block_m;
-        int lo = 0, hi = NB;  // first bucket with pend > row
-        while (lo < hi) {
-            int mid = (lo + hi) >> 1;
-            if (pend[mid] > row) hi = mid; else lo = mid + 1;
-        }
-        expert_ids[tl] = lo < E ? lo : -1;
-    }
+    for (int64_t tl = used / block_m + (int64_t)slice * kThreads + tid; tl < tiles; tl += stride)
+        expert_ids[tl] = -1;
     if (slice == 0 && tid == 0) total[0] = used;
 }
 

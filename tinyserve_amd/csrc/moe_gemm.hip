@@ -22,21 +22,6 @@ namespace {
 constexpr int BK = 64;        // K elements per main-loop step
 constexpr int LDK = BK + 8;   // LDS row stride in bf16 elements (144 bytes: 16-byte aligned rows)
 
-struct GemmArgs {
-    const bf16_t* A;            // gate_up: x [T, K]; down: act [max_padded, K]
-    const bf16_t* B;            // gate_up: w13 [E, 2N, K]; down: w2 [E, N, K]
-    bf16_t* C;                  // gate_up: act [max_padded, N]; down: rows [numel, N]
-    const float* topk_w;        // down only: [numel]
-    const int32_t* sorted_ids;  // [max_padded]
-    const int32_t* expert_ids;  // [max_padded / BM]
-    const int32_t* total;       // [1]
-    int64_t numel;
-    int top_k;
-    int N;                      // output columns (gate_up: I; down: H)
-    int K;                      // reduction length (gate_up: H; down: I)
-    int m_tiles;
-    int n_tiles;
-};
 
 // bf16(silu(g)) * u with g, u first rounded to bf16 (the reference stores gate/up as bf16).
 __device__ __forceinline__ float swiglu(float g, float u) {
@@ -49,7 +34,7 @@ __device__ __forceinline__ float swiglu(float g, float u) {
 // Workgroup tile BM x BN of C (for gate_up, BN counts B rows: BN/2 gate rows + the matching BN/2
 // up rows, so BN/2 activation columns), 4 wavefronts in a WM x WN grid, 16x16x32 bf16 MFMA,
 // A and B staged through double-buffered LDS with a register prefetch of the next K step.
-template <int BM, int BN, int WM, int WN, bool GATEUP>
+template <int BM, int BN, int WM, int WN, bool GATEUP, bool PACKED>
 __global__ __launch_bounds__(256) void moe_gemm_kernel(GemmArgs p) {
     constexpr int WTM = BM / WM, WTN = BN / WN;
     constexpr int FM = WTM / 16, FN = WTN / 16;
@@ -113,8 +98,16 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(GemmArgs p) {
             brow = row < BN / 2 ? n_tile * (BN / 2) + row : p.N + n_tile * (BN / 2) + row - BN / 2;
         else
             brow = n_tile * BN + row;
-        b_src[c] = Be + (int64_t)brow * p.K + kc * 8;
+        if (PACKED) {  // MFMA-tiled layout (moe_pack.hip); w13 blocks interleave gate/up
+            const int blk = GATEUP ? (brow < p.N ? 2 * (brow >> 4) : 2 * ((brow - p.N) >> 4) + 1)
+                                   : (brow >> 4);
+            b_src[c] = Be + (((int64_t)blk * (p.K / 32) + (kc >> 2)) * 64 + (brow & 15) +
+                             16 * (kc & 3)) * 8;
+        } else {
+            b_src[c] = Be + (int64_t)brow * p.K + kc * 8;
+        }
     }
+    constexpr int kBStep = PACKED ? (BK / 32) * 512 : BK;  // elements per K step
 
     u32x4 ra[CA], rb[CB];
     auto gload = [&](int kt) {
@@ -123,7 +116,8 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(GemmArgs p) {
             ra[c] = a_src[c] ? *reinterpret_cast<const u32x4*>(a_src[c] + kt * BK)
                              : u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
-        for (int c = 0; c < CB; ++c) rb[c] = *reinterpret_cast<const u32x4*>(b_src[c] + kt * BK);
+        for (int c = 0; c < CB; ++c)
+            rb[c] = *reinterpret_cast<const u32x4*>(b_src[c] + kt * kBStep);
     };
     auto sstore = [&](int buf) {
 #pragma unroll
@@ -332,29 +326,40 @@ GemmArgs gemm_args(const bf16_t* A, const bf16_t* B, bf16_t* C, const float* top
 bool block_m_supported(int block_m) { return block_m == 16 || block_m == 64; }
 
 // gate_up GEMM + SwiGLU: act[max_padded, I] from x[T, H] and w13[E, 2I, H].
+template <int BM, int WM, int WN, bool GATEUP>
+void launch_lds(const GemmArgs& g, bool packed, hipStream_t stream) {
+    const dim3 grid(g.m_tiles * g.n_tiles);
+    if (packed)
+        hipLaunchKernelGGL((moe_gemm_kernel<BM, kBN, WM, WN, GATEUP, true>), grid, dim3(256), 0,
+                           stream, g);
+    else
+        hipLaunchKernelGGL((moe_gemm_kernel<BM, kBN, WM, WN, GATEUP, false>), grid, dim3(256), 0,
+                           stream, g);
+}
+
 void launch_gate_up(const bf16_t* x, const bf16_t* w13, const int32_t* sorted,
                     const int32_t* eids, const int32_t* total, int64_t numel, int top_k, int H,
-                    int I, int E, int block_m, bf16_t* act, hipStream_t stream) {
+                    int I, int E, int block_m, bool packed, bf16_t* act, hipStream_t stream) {
     GemmArgs g = gemm_args(x, w13, act, nullptr, sorted, eids, total, numel, top_k, I, H, E,
                            block_m, I / (kBN / 2));
-    const dim3 grid(g.m_tiles * g.n_tiles);
+    if (block_m == 16 && launch_stream_gate_up(g, packed, stream)) return;
     if (block_m == 16)
-        hipLaunchKernelGGL((moe_gemm_kernel<16, kBN, 1, 4, true>), grid, dim3(256), 0, stream, g);
+        launch_lds<16, 1, 4, true>(g, packed, stream);
     else
-        hipLaunchKernelGGL((moe_gemm_kernel<64, kBN, 2, 2, true>), grid, dim3(256), 0, stream, g);
+        launch_lds<64, 2, 2, true>(g, packed, stream);
 }
 
 // down GEMM * routing weight: rows[numel, H] from act[max_padded, I] and w2[E, H, I].
 void launch_down(const bf16_t* act, const bf16_t* w2, const float* topk_w, const int32_t* sorted,
                  const int32_t* eids, const int32_t* total, int64_t numel, int H, int I, int E,
-                 int block_m, bf16_t* rows, hipStream_t stream) {
+                 int block_m, bool packed, bf16_t* rows, hipStream_t stream) {
     GemmArgs g = gemm_args(act, w2, rows, topk_w, sorted, eids, total, numel, 1, H, I, E,
                            block_m, H / kBN);
-    const dim3 grid(g.m_tiles * g.n_tiles);
+    if (block_m == 16 && launch_stream_down(g, packed, stream)) return;
     if (block_m == 16)
-        hipLaunchKernelGGL((moe_gemm_kernel<16, kBN, 1, 4, false>), grid, dim3(256), 0, stream, g);
+        launch_lds<16, 1, 4, false>(g, packed, stream);
     else
-        hipLaunchKernelGGL((moe_gemm_kernel<64, kBN, 2, 2, false>), grid, dim3(256), 0, stream, g);
+        launch_lds<64, 2, 2, false>(g, packed, stream);
 }
 
 void launch_combine(const bf16_t* rows, int64_t T, int H, int top_k, bf16_t* out,
@@ -367,7 +372,7 @@ void launch_combine(const bf16_t* rows, int64_t T, int H, int top_k, bf16_t* out
 // Everything after routing: align, gate_up + SwiGLU, down * weight, k-sum.
 int run_experts(const void* x, const void* w13, const void* w2, const float* topk_w,
                 const int32_t* topk_ids, int64_t T, int H, int I, int E, int top_k, int sum_topk,
-                void* out, char* ws, const Layout& L, hipStream_t stream) {
+                bool packed, void* out, char* ws, const Layout& L, hipStream_t stream) {
     const Plan pl = plan_for(T, E, top_k);
     const int64_t numel = T * top_k;
     int32_t* sorted = reinterpret_cast<int32_t*>(ws + L.sorted);
@@ -378,9 +383,9 @@ int run_experts(const void* x, const void* w13, const void* w2, const float* top
 
     (void)launch_align(topk_ids, numel, E, pl.block_m, sorted, eids, total, ws + L.hist, stream);
     launch_gate_up((const bf16_t*)x, (const bf16_t*)w13, sorted, eids, total, numel, top_k, H, I,
-                   E, pl.block_m, act, stream);
+                   E, pl.block_m, packed, act, stream);
     launch_down(act, (const bf16_t*)w2, topk_w, sorted, eids, total, numel, H, I, E, pl.block_m,
-                rows, stream);
+                packed, rows, stream);
     if (sum_topk) launch_combine(rows, T, H, top_k, (bf16_t*)out, stream);
     return check_launch("fused_moe kernels");
 }
@@ -420,10 +425,10 @@ extern "C" size_t tsm_fused_moe_workspace_size(int64_t T, int H, int I, int E, i
     return layout_for(T, H, I, E, top_k, false).bytes;
 }
 
-extern "C" int tsm_fused_moe(const void* x, const void* w13, const void* w2, const float* topk_w,
-                             const int32_t* topk_ids, int64_t T, int H, int I, int E, int top_k,
-                             int sum_topk, void* out, void* ws, size_t ws_bytes,
-                             hipStream_t stream) {
+static int fused_moe_impl(const void* x, const void* w13, const void* w2, const float* topk_w,
+                          const int32_t* topk_ids, int64_t T, int H, int I, int E, int top_k,
+                          int sum_topk, bool packed, void* out, void* ws, size_t ws_bytes,
+                          hipStream_t stream) {
     clear_error();
     int rc = check_moe_shapes(T, H, I, E, top_k);
     if (rc) return rc;
@@ -433,8 +438,24 @@ extern "C" int tsm_fused_moe(const void* x, const void* w13, const void* w2, con
     TSM_REQUIRE(ws && ws_bytes >= L.bytes && ((uintptr_t)ws & 255) == 0, TSM_E_WORKSPACE,
                 "workspace must be 256-byte aligned and >= %zu bytes (got %zu)", L.bytes,
                 ws_bytes);
-    return run_experts(x, w13, w2, topk_w, topk_ids, T, H, I, E, top_k, sum_topk, out,
+    return run_experts(x, w13, w2, topk_w, topk_ids, T, H, I, E, top_k, sum_topk, packed, out,
                        (char*)ws, L, stream);
+}
+
+extern "C" int tsm_fused_moe(const void* x, const void* w13, const void* w2, const float* topk_w,
+                             const int32_t* topk_ids, int64_t T, int H, int I, int E, int top_k,
+                             int sum_topk, void* out, void* ws, size_t ws_bytes,
+                             hipStream_t stream) {
+    return fused_moe_impl(x, w13, w2, topk_w, topk_ids, T, H, I, E, top_k, sum_topk, false, out,
+                          ws, ws_bytes, stream);
+}
+
+extern "C" int tsm_fused_moe_packed(const void* x, const void* w13p, const void* w2p,
+                                    const float* topk_w, const int32_t* topk_ids, int64_t T, int H,
+                                    int I, int E, int top_k, int sum_topk, void* out, void* ws,
+                                    size_t ws_bytes, hipStream_t stream) {
+    return fused_moe_impl(x, w13p, w2p, topk_w, topk_ids, T, H, I, E, top_k, sum_topk, true, out,
+                          ws, ws_bytes, stream);
 }
 
 extern "C" size_t tsm_moe_forward_workspace_size(int64_t T, int H, int I, int E, int top_k) {
@@ -442,11 +463,11 @@ extern "C" size_t tsm_moe_forward_workspace_size(int64_t T, int H, int I, int E,
     return layout_for(T, H, I, E, top_k, true).bytes;
 }
 
-extern "C" int tsm_moe_forward(const void* x, const void* gate_w, const void* w13, const void* w2,
-                               const int64_t* expert_map, const float* bias, int64_t T, int H,
-                               int I, int E, int top_k, int renorm, int logits_bf16,
-                               int sum_topk, void* out, float* topk_w, int32_t* topk_ids,
-                               void* ws, size_t ws_bytes, hipStream_t stream) {
+static int moe_forward_impl(const void* x, const void* gate_w, const void* w13, const void* w2,
+                            const int64_t* expert_map, const float* bias, int64_t T, int H, int I,
+                            int E, int top_k, int renorm, int logits_bf16, int sum_topk,
+                            bool packed, void* out, float* topk_w, int32_t* topk_ids, void* ws,
+                            size_t ws_bytes, hipStream_t stream) {
     clear_error();
     int rc = check_moe_shapes(T, H, I, E, top_k);
     if (rc) return rc;
@@ -462,13 +483,35 @@ extern "C" int tsm_moe_forward(const void* x, const void* gate_w, const void* w1
     rc = tsm_moe_router(x, gate_w, TSM_BF16, T, H, E, top_k, renorm, expert_map, bias,
                         logits_bf16, nullptr, tw, ti, stream);
     if (rc) return rc;
-    return run_experts(x, w13, w2, tw, ti, T, H, I, E, top_k, sum_topk, out, w, L, stream);
+    return run_experts(x, w13, w2, tw, ti, T, H, I, E, top_k, sum_topk, packed, out, w, L,
+                       stream);
+}
+
+extern "C" int tsm_moe_forward(const void* x, const void* gate_w, const void* w13, const void* w2,
+                               const int64_t* expert_map, const float* bias, int64_t T, int H,
+                               int I, int E, int top_k, int renorm, int logits_bf16,
+                               int sum_topk, void* out, float* topk_w, int32_t* topk_ids,
+                               void* ws, size_t ws_bytes, hipStream_t stream) {
+    return moe_forward_impl(x, gate_w, w13, w2, expert_map, bias, T, H, I, E, top_k, renorm,
+                            logits_bf16, sum_topk, false, out, topk_w, topk_ids, ws, ws_bytes,
+                            stream);
+}
+
+extern "C" int tsm_moe_forward_packed(const void* x, const void* gate_w, const void* w13p,
+                                      const void* w2p, const int64_t* expert_map,
+                                      const float* bias, int64_t T, int H, int I, int E,
+                                      int top_k, int renorm, int logits_bf16, int sum_topk,
+                                      void* out, float* topk_w, int32_t* topk_ids, void* ws,
+                                      size_t ws_bytes, hipStream_t stream) {
+    return moe_forward_impl(x, gate_w, w13p, w2p, expert_map, bias, T, H, I, E, top_k, renorm,
+                            logits_bf16, sum_topk, true, out, topk_w, topk_ids, ws, ws_bytes,
+                            stream);
 }
 
 extern "C" int tsm_moe_gemm_gate_up(const void* x, const void* w13, const int32_t* sorted_ids,
                                     const int32_t* expert_ids, const int32_t* total,
                                     int64_t numel, int top_k, int H, int I, int E, int block_m,
-                                    void* act, hipStream_t stream) {
+                                    int weight_layout, void* act, hipStream_t stream) {
     clear_error();
     int rc = check_moe_shapes(numel / (top_k > 0 ? top_k : 1), H, I, E, top_k);
     if (rc) return rc;
@@ -478,14 +521,15 @@ extern "C" int tsm_moe_gemm_gate_up(const void* x, const void* w13, const int32_
     TSM_REQUIRE(x && w13 && sorted_ids && expert_ids && total && act, TSM_E_ARG,
                 "null pointer argument");
     launch_gate_up((const bf16_t*)x, (const bf16_t*)w13, sorted_ids, expert_ids, total, numel,
-                   top_k, H, I, E, block_m, (bf16_t*)act, stream);
+                   top_k, H, I, E, block_m, weight_layout != 0, (bf16_t*)act, stream);
     return check_launch("gate_up GEMM");
 }
 
 extern "C" int tsm_moe_gemm_down(const void* act, const void* w2, const float* topk_w,
                                  const int32_t* sorted_ids, const int32_t* expert_ids,
                                  const int32_t* total, int64_t numel, int H, int I, int E,
-                                 int block_m, void* rows, hipStream_t stream) {
+                                 int block_m, int weight_layout, void* rows,
+                                 hipStream_t stream) {
     clear_error();
     int rc = check_moe_shapes(numel, H, I, E, 1);
     if (rc) return rc;
@@ -495,7 +539,7 @@ extern "C" int tsm_moe_gemm_down(const void* act, const void* w2, const float* t
     TSM_REQUIRE(act && w2 && topk_w && sorted_ids && expert_ids && total && rows, TSM_E_ARG,
                 "null pointer argument");
     launch_down((const bf16_t*)act, (const bf16_t*)w2, topk_w, sorted_ids, expert_ids, total,
-                numel, H, I, E, block_m, (bf16_t*)rows, stream);
+                numel, H, I, E, block_m, weight_layout != 0, (bf16_t*)rows, stream);
     return check_launch("down GEMM");
 }
 

@@ -100,17 +100,36 @@ __global__ __launch_bounds__(256) void route_logits_kernel(
     wave_select(v, E, top_k, renorm, expert_map, topk_w + t * top_k, topk_ids + t * top_k);
 }
 
-// Eight consecutive inputs starting at p (16-byte aligned for bf16, 32-byte for fp32) as fp32.
-__device__ __forceinline__ void load8(const bf16_t* p, float (&o)[8]) {
-    u32x4 w = *reinterpret_cast<const u32x4*>(p);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) { o[2 * i] = lo_bf16(w[i]); o[2 * i + 1] = hi_bf16(w[i]); }
-}
-__device__ __forceinline__ void load8(const float* p, float (&o)[8]) {
-    float4 a = reinterpret_cast<const float4*>(p)[0];
-    float4 b = reinterpret_cast<const float4*>(p)[1];
-    o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w; o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
-}
+// Eight consecutive inputs (16 bytes of bf16 or 32 bytes of fp32), kept raw until used.
+template <typename TIn>
+struct Chunk8;
+template <>
+struct Chunk8<bf16_t> {
+    u32x4 v;
+    __device__ __forceinline__ void load(const bf16_t* p) { v = *reinterpret_cast<const u32x4*>(p); }
+    __device__ __forceinline__ void zero() { v = u32x4{0u, 0u, 0u, 0u}; }
+    __device__ __forceinline__ float get(int i) const {
+        return (i & 1) ? hi_bf16(v[i >> 1]) : lo_bf16(v[i >> 1]);
+    }
+};
+template <>
+struct Chunk8<float> {
+    float4 a, b;
+    __device__ __forceinline__ void load(const float* p) {
+        a = reinterpret_cast<const float4*>(p)[0];
+        b = reinterpret_cast<const float4*>(p)[1];
+    }
+    __device__ __forceinline__ void zero() { a = b = make_float4(0.f, 0.f, 0.f, 0.f); }
+    __device__ __forceinline__ float get(int i) const {
+        const float4& h = i < 4 ? a : b;
+        switch (i & 3) {
+            case 0: return h.x;
+            case 1: return h.y;
+            case 2: return h.z;
+            default: return h.w;
+        }
+    }
+};
 
 // Gate GEMM + routing. Workgroup = kRouterWaves wavefronts and TB tokens; each wavefront computes
 // the logits of experts e = wave, wave + kRouterWaves, ... for the TB tokens (x slice held in
@@ -134,40 +153,53 @@ __global__ __launch_bounds__(kRouterWaves * 64) void router_kernel(
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
             const int h0 = c * 512 + lane * 8;
-            float tmp[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-            if (h0 < H && t0 + tb < T) load8(x + (t0 + tb) * H + h0, tmp);
+            Chunk8<TIn> ch;
+            ch.zero();
+            if (h0 < H && t0 + tb < T) ch.load(x + (t0 + tb) * H + h0);
 #pragma unroll
-            for (int i = 0; i < 8; ++i) xr[tb][c * 8 + i] = tmp[i];
+            for (int i = 0; i < 8; ++i) xr[tb][c * 8 + i] = ch.get(i);
         }
     }
 
-    for (int e = wave; e < E; e += kRouterWaves) {
-        float g[NC * 8];
+    // Experts e0 + j*kRouterWaves (j < GE) are in flight together: all their loads are issued
+    // before the first multiply.
+    constexpr int kWords = sizeof(TIn) * 2;  // VGPRs per raw 8-element chunk
+    constexpr int kGe = ((TB == 1 ? 96 : 80) - TB * NC * 8) / (NC * kWords);
+    constexpr int GE = kGe < 1 ? 1 : (kGe > 4 ? 4 : kGe);
+    for (int e0 = wave; e0 < E; e0 += kRouterWaves * GE) {
+        Chunk8<TIn> gc[GE][NC];
 #pragma unroll
-        for (int c = 0; c < NC; ++c) {
-            const int h0 = c * 512 + lane * 8;
-            float tmp[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-            if (h0 < H) load8(gw + (int64_t)e * H + h0, tmp);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) g[c * 8 + i] = tmp[i];
-        }
-#pragma unroll
-        for (int tb = 0; tb < TB; ++tb) {
-            float acc = 0.0f;
+        for (int j = 0; j < GE; ++j) {
+            const int e = e0 + j * kRouterWaves;
 #pragma unroll
             for (int c = 0; c < NC; ++c) {
-                if (c * 512 + lane * 8 < H) {
-#pragma unroll
-                    for (int i = 0; i < 8; ++i)
-                        acc = __builtin_fmaf(xr[tb][c * 8 + i], g[c * 8 + i], acc);
-                }
+                const int h0 = c * 512 + lane * 8;
+                gc[j][c].zero();
+                if (e < E && h0 < H) gc[j][c].load(gw + (int64_t)e * H + h0);
             }
-            float l = wave_sum_butterfly(acc);
-            if (bias) l = l + bias[e];
-            if (logits_bf16) l = round_bf16(l);
-            if (lane == 0) {
-                s_logits[tb * E + e] = l;
-                if (logits_out && t0 + tb < T) logits_out[(t0 + tb) * E + e] = l;
+        }
+#pragma unroll
+        for (int j = 0; j < GE; ++j) {
+            const int e = e0 + j * kRouterWaves;
+            if (e >= E) break;
+#pragma unroll
+            for (int tb = 0; tb < TB; ++tb) {
+                float acc = 0.0f;
+#pragma unroll
+                for (int c = 0; c < NC; ++c) {
+                    if (c * 512 + lane * 8 < H) {
+#pragma unroll
+                        for (int i = 0; i < 8; ++i)
+                            acc = __builtin_fmaf(xr[tb][c * 8 + i], gc[j][c].get(i), acc);
+                    }
+                }
+                float l = wave_sum_butterfly(acc);
+                if (bias) l = l + bias[e];
+                if (logits_bf16) l = round_bf16(l);
+                if (lane == 0) {
+                    s_logits[tb * E + e] = l;
+                    if (logits_out && t0 + tb < T) logits_out[(t0 + tb) * E + e] = l;
+                }
             }
         }
     }

@@ -9,6 +9,8 @@ DecoderLayer that calls `self.mlp(h)` are unchanged:
 `forward` runs the fused router (gate GEMM + fp32 softmax/top-k/renormalise, one launch) and the
 experts (align, gate_up+SwiGLU, down, k-sum). With `router="linear"` it instead computes the
 logits with self.gate (bf16, as the reference does) and routes them with moe_route.
+With `packed=True` (default) the experts run on an MFMA-tiled copy of w13/w2 (pack_moe_weights),
+made on the first forward after the parameters change (call `pack()` before HIP-graph capture).
 Tensor parallelism is not part of this build: the result is this GPU's share (what the reference
 passes to tp_all_reduce).
 """
@@ -19,7 +21,7 @@ from . import ops
 
 
 class SparseMoE(nn.Module):
-    def __init__(self, cfg, router: str = "fused"):
+    def __init__(self, cfg, router: str = "fused", packed: bool = True):
         super().__init__()
         E, H, I = cfg.num_experts, cfg.hidden_size, cfg.moe_intermediate_size
         self.top_k = cfg.num_experts_per_tok
@@ -36,6 +38,19 @@ class SparseMoE(nn.Module):
         if router not in ("fused", "linear"):
             raise ValueError("router must be 'fused' or 'linear'")
         self.router = router
+        self.packed = packed
+        self._packed_key = None
+        self._w13_packed = None
+        self._w2_packed = None
+
+    def pack(self):
+        """(Re)build the MFMA-tiled weight copies if w13/w2 changed since the last pack."""
+        key = (self.w13.data_ptr(), self.w2.data_ptr(), self.w13._version, self.w2._version)
+        if key != self._packed_key:
+            with torch.no_grad():
+                self._w13_packed, self._w2_packed = ops.pack_moe_weights(self.w13, self.w2)
+            self._packed_key = key
+        return self._w13_packed, self._w2_packed
 
     def load_expert(self, expert: int, proj: str, fh, key: str, rank: int = 0,
                     tp: int = 1) -> bool:
@@ -58,6 +73,14 @@ class SparseMoE(nn.Module):
         return True
 
     def forward(self, x):
+        if self.packed:
+            w13, w2 = self.pack()
+            if self.router == "fused":
+                return ops.moe_forward_packed(x, self.gate.weight, w13, w2, self.top_k,
+                                              self.norm_topk_prob, self.expert_map)
+            topk_weights, topk_ids = ops.moe_route(self.gate(x), self.top_k,
+                                                   self.norm_topk_prob, self.expert_map)
+            return ops.fused_moe_packed(x, w13, w2, topk_weights, topk_ids)
         if self.router == "fused":
             return ops.moe_forward(x, self.gate.weight, self.w13, self.w2, self.top_k,
                                    self.norm_topk_prob, self.expert_map)

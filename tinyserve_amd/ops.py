@@ -167,10 +167,7 @@ def _check_weights(x, w13, w2):
     return T, H, E, I
 
 
-@torch.library.custom_op("tinyserve_amd::fused_moe", mutates_args=())
-def fused_moe(x: Tensor, w13: Tensor, w2: Tensor, topk_weights: Tensor, topk_ids: Tensor,
-              sum_topk: bool = True) -> Tensor:
-    """sum_k weight_k * expert_k(x) -> [T, H] (or the per-slot rows [T*k, H])."""
+def _fused_moe_impl(x, w13, w2, topk_weights, topk_ids, sum_topk, packed):
     _on_gpu(x, w13, w2, topk_weights, topk_ids)
     x, w13, w2 = _contig(x), _contig(w13), _contig(w2)
     T, H, E, I = _check_weights(x, w13, w2)
@@ -180,9 +177,17 @@ def fused_moe(x: Tensor, w13: Tensor, w2: Tensor, topk_weights: Tensor, topk_ids
     out = torch.empty((T, H) if sum_topk else (T * k, H), dtype=x.dtype, device=x.device)
     nws = int(lib.tsm_fused_moe_workspace_size(T, H, I, E, k))
     ws = torch.empty(max(nws, 1), dtype=torch.uint8, device=x.device)
-    check(lib.tsm_fused_moe(ptr(x), ptr(w13), ptr(w2), ptr(tw), ptr(ti), T, H, I, E, k,
-                            int(sum_topk), ptr(out), ptr(ws), nws, stream_of(x)), "fused_moe")
+    fn = lib.tsm_fused_moe_packed if packed else lib.tsm_fused_moe
+    check(fn(ptr(x), ptr(w13), ptr(w2), ptr(tw), ptr(ti), T, H, I, E, k, int(sum_topk), ptr(out),
+             ptr(ws), nws, stream_of(x)), "fused_moe")
     return out
+
+
+@torch.library.custom_op("tinyserve_amd::fused_moe", mutates_args=())
+def fused_moe(x: Tensor, w13: Tensor, w2: Tensor, topk_weights: Tensor, topk_ids: Tensor,
+              sum_topk: bool = True) -> Tensor:
+    """sum_k weight_k * expert_k(x) -> [T, H] (or the per-slot rows [T*k, H])."""
+    return _fused_moe_impl(x, w13, w2, topk_weights, topk_ids, sum_topk, False)
 
 
 @fused_moe.register_fake
@@ -192,12 +197,46 @@ def _(x, w13, w2, topk_weights, topk_ids, sum_topk=True):
     return x.new_empty((T, H) if sum_topk else (T * k, H))
 
 
-@torch.library.custom_op("tinyserve_amd::moe_forward", mutates_args=())
-def moe_forward(x: Tensor, gate_w: Tensor, w13: Tensor, w2: Tensor, top_k: int,
-                renormalize: bool, expert_map: Optional[Tensor] = None,
-                bias: Optional[Tensor] = None, logits_bf16: bool = False,
-                sum_topk: bool = True) -> Tensor:
-    """Whole MoE block: fused router (gate GEMM + softmax/top-k) then the experts."""
+@torch.library.custom_op("tinyserve_amd::fused_moe_packed", mutates_args=())
+def fused_moe_packed(x: Tensor, w13_packed: Tensor, w2_packed: Tensor, topk_weights: Tensor,
+                     topk_ids: Tensor, sum_topk: bool = True) -> Tensor:
+    """fused_moe on weights reordered by pack_moe_weights (same shapes as w13 / w2)."""
+    return _fused_moe_impl(x, w13_packed, w2_packed, topk_weights, topk_ids, sum_topk, True)
+
+
+@fused_moe_packed.register_fake
+def _(x, w13_packed, w2_packed, topk_weights, topk_ids, sum_topk=True):
+    T, H = x.shape
+    k = topk_ids.shape[1]
+    return x.new_empty((T, H) if sum_topk else (T * k, H))
+
+
+@torch.library.custom_op("tinyserve_amd::pack_moe_weights", mutates_args=())
+def pack_moe_weights(w13: Tensor, w2: Tensor) -> Tuple[Tensor, Tensor]:
+    """MFMA-tiled copies of w13 [E, 2I, H] and w2 [E, H, I] (same shapes and sizes); one-time,
+    at weight-load time. Their contents are only meaningful to the *_packed ops."""
+    _on_gpu(w13, w2)
+    if w13.dtype != torch.bfloat16 or w2.dtype != torch.bfloat16:
+        raise TypeError("packing supports bf16 weights")
+    w13, w2 = _contig(w13), _contig(w2)
+    E, two_i, H = w13.shape
+    I = two_i // 2
+    if tuple(w2.shape) != (E, H, I):
+        raise ValueError(f"w2 {tuple(w2.shape)} does not match w13 {tuple(w13.shape)}")
+    p13, p2 = torch.empty_like(w13), torch.empty_like(w2)
+    s = stream_of(w13)
+    check(lib.tsm_moe_pack_weights(ptr(w13), E, two_i, H, 1, ptr(p13), s), "pack w13")
+    check(lib.tsm_moe_pack_weights(ptr(w2), E, H, I, 0, ptr(p2), s), "pack w2")
+    return p13, p2
+
+
+@pack_moe_weights.register_fake
+def _(w13, w2):
+    return torch.empty_like(w13), torch.empty_like(w2)
+
+
+def _moe_forward_impl(x, gate_w, w13, w2, top_k, renormalize, expert_map, bias, logits_bf16,
+                      sum_topk, packed):
     _on_gpu(x, gate_w, w13, w2, expert_map, bias)
     x, gate_w, w13, w2 = _contig(x), _contig(gate_w), _contig(w13), _contig(w2)
     T, H, E, I = _check_weights(x, w13, w2)
@@ -208,14 +247,42 @@ def moe_forward(x: Tensor, gate_w: Tensor, w13: Tensor, w2: Tensor, top_k: int,
     out = torch.empty((T, H) if sum_topk else (T * top_k, H), dtype=x.dtype, device=x.device)
     nws = int(lib.tsm_moe_forward_workspace_size(T, H, I, E, top_k))
     ws = torch.empty(max(nws, 1), dtype=torch.uint8, device=x.device)
-    check(lib.tsm_moe_forward(ptr(x), ptr(gate_w), ptr(w13), ptr(w2), ptr(m), ptr(b), T, H, I, E,
-                              top_k, int(renormalize), int(logits_bf16), int(sum_topk), ptr(out),
-                              None, None, ptr(ws), nws, stream_of(x)), "moe_forward")
+    fn = lib.tsm_moe_forward_packed if packed else lib.tsm_moe_forward
+    check(fn(ptr(x), ptr(gate_w), ptr(w13), ptr(w2), ptr(m), ptr(b), T, H, I, E, top_k,
+             int(renormalize), int(logits_bf16), int(sum_topk), ptr(out), None, None, ptr(ws),
+             nws, stream_of(x)), "moe_forward")
     return out
+
+
+@torch.library.custom_op("tinyserve_amd::moe_forward", mutates_args=())
+def moe_forward(x: Tensor, gate_w: Tensor, w13: Tensor, w2: Tensor, top_k: int,
+                renormalize: bool, expert_map: Optional[Tensor] = None,
+                bias: Optional[Tensor] = None, logits_bf16: bool = False,
+                sum_topk: bool = True) -> Tensor:
+    """Whole MoE block: fused router (gate GEMM + softmax/top-k) then the experts."""
+    return _moe_forward_impl(x, gate_w, w13, w2, top_k, renormalize, expert_map, bias,
+                             logits_bf16, sum_topk, False)
 
 
 @moe_forward.register_fake
 def _(x, gate_w, w13, w2, top_k, renormalize, expert_map=None, bias=None, logits_bf16=False,
       sum_topk=True):
+    T, H = x.shape
+    return x.new_empty((T, H) if sum_topk else (T * top_k, H))
+
+
+@torch.library.custom_op("tinyserve_amd::moe_forward_packed", mutates_args=())
+def moe_forward_packed(x: Tensor, gate_w: Tensor, w13_packed: Tensor, w2_packed: Tensor,
+                       top_k: int, renormalize: bool, expert_map: Optional[Tensor] = None,
+                       bias: Optional[Tensor] = None, logits_bf16: bool = False,
+                       sum_topk: bool = True) -> Tensor:
+    """moe_forward on weights reordered by pack_moe_weights."""
+    return _moe_forward_impl(x, gate_w, w13_packed, w2_packed, top_k, renormalize, expert_map,
+                             bias, logits_bf16, sum_topk, True)
+
+
+@moe_forward_packed.register_fake
+def _(x, gate_w, w13_packed, w2_packed, top_k, renormalize, expert_map=None, bias=None,
+      logits_bf16=False, sum_topk=True):
     T, H = x.shape
     return x.new_empty((T, H) if sum_topk else (T * top_k, H))
