@@ -145,7 +145,7 @@ def main():
         launch stream. Returns mean ms per stage launch."""
         xs = inputs(T, 1000 + T)
         numel = T * K_TOP
-        bm = int(lib.tsm_moe_block_m(T, H, I, E, K_TOP))
+        bm = int(lib.tsm_moe_block_m(T, H, I, E, K_TOP, 1))
         mp = int(lib.tsm_moe_max_padded(numel, E, bm))
         w = torch.empty(T, K_TOP, dtype=torch.float32, device=dev)
         ids = torch.empty(T, K_TOP, dtype=torch.int32, device=dev)
@@ -215,7 +215,7 @@ def main():
     dom_t = stages_ms[dom] * 1e-3
     roofline = {
         "kernel": "moe_stream_kernel<gate_up, packed> (gate_up GEMM + SwiGLU epilogue)"
-                  if bm == 16 else "moe_gemm_kernel<gate_up, packed> (gate_up GEMM + SwiGLU)",
+                  if bm == 16 else "moe_tile_kernel<gate_up> (gate_up GEMM + SwiGLU epilogue)",
         "bound": "hbm",
         "achieved": sb[dom] / dom_t / 1e9,
         "peak": HBM_PEAK / 1e9,

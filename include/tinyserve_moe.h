@@ -102,10 +102,11 @@ int tsm_silu_and_mul(const void* gate, int64_t gate_stride, const void* up, int6
                      void* out, int64_t out_stride, int64_t rows, int64_t N, hipStream_t stream);
 
 /*
- * Tile height (rows per expert tile) fused_moe uses for a batch of T tokens. The reference picks
- * 16 when T*k <= 4E, else 64 (tinykernels.py:1779); this build picks from its own kernel table.
+ * Tile height (rows per expert tile) fused_moe uses for a batch of T tokens with the given weight
+ * layout (TSM_LAYOUT_*). The reference picks 16 when T*k <= 4E, else 64 (tinykernels.py:1779);
+ * this build picks from its own kernel table (16 / 64, and 128 for packed weights).
  */
-int tsm_moe_block_m(int64_t T, int H, int I, int E, int top_k);
+int tsm_moe_block_m(int64_t T, int H, int I, int E, int top_k, int weight_layout);
 
 /*
  * Experts on sorted rows: align + grouped gate_up GEMM with the SwiGLU epilogue + grouped down GEMM
@@ -124,7 +125,7 @@ int tsm_fused_moe(const void* x, const void* w13, const void* w2, const float* t
  * The stages of tsm_fused_moe, for callers that schedule them separately (and for per-kernel
  * timing). Each is one launch of the corresponding stage of _moe_gemm / _fused_moe_kernel
  * (tinykernels.py:1746-1765, 1589-1744) on the outputs of tsm_moe_align for the same block_m
- * (supported: 16, 64):
+ * (supported: 16, 64; 128 with packed weights):
  *   gate_up: act[max_padded, I] (expert-sorted rows) = bf16(bf16(silu(bf16(x W1^T))) *
  *            bf16(x W3^T)) with x gathered as x[sorted_ids[r] / top_k]; rows of remote tiles
  *            are not written.

@@ -35,5 +35,20 @@ struct GemmArgs {
 bool launch_stream_gate_up(GemmArgs g, bool packed, hipStream_t stream);
 bool launch_stream_down(GemmArgs g, bool packed, hipStream_t stream);
 
+// Upper bound on the tiles the align step can fill, whatever the routing: bucket b with c_b rows
+// fills ceil(c_b / bm) <= c_b / bm + 1 tiles, and at most min(numel, E + 1) buckets are
+// non-empty. GEMM grids are sized by this bound (static, so graph-capturable), not by
+// max_padded / bm, which matters when numel is small.
+inline int64_t active_tile_bound(int64_t numel, int E, int block_m) {
+    const int64_t all = max_padded_rows(numel, E, block_m) / block_m;
+    const int64_t nonempty = numel < E + 1 ? numel : E + 1;
+    const int64_t bound = (numel + block_m - 1) / block_m + nonempty;
+    return bound < all ? bound : all;
+}
+
+// LDS-pipelined kernels for 64/128-row tiles on packed weights; false if unsupported.
+bool launch_tile_gate_up(GemmArgs g, int block_m, hipStream_t stream);
+bool launch_tile_down(GemmArgs g, int block_m, hipStream_t stream);
+
 inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 }  // namespace tsm

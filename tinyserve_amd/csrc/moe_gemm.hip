@@ -249,17 +249,18 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const bf16_t* __restrict_
 }
 
 // ---- kernel table --------------------------------------------------------------------------
-enum Variant { kDecode = 0, kPrefill = 1 };
-
+// Tile height per batch size. Reference-layout weights: 16-row weight-streaming tiles while
+// numel <= 4E (the reference's own BLOCK_M switch, tinykernels.py:1779), else 64-row LDS tiles.
+// Packed weights: 16-row tiles up to 4E, 64-row pipelined tiles up to 32E, 128-row above.
 struct Plan {
     int block_m;
-    Variant v;
 };
 
-Plan plan_for(int64_t T, int E, int top_k) {
+Plan plan_for(int64_t T, int E, int top_k, bool packed) {
     const int64_t numel = T * top_k;
-    if (numel <= 4ll * E) return Plan{16, kDecode};
-    return Plan{64, kPrefill};
+    if (numel <= 4ll * E) return Plan{16};
+    if (!packed || numel <= 32ll * E) return Plan{64};
+    return Plan{128};
 }
 
 constexpr int kBN = 128;  // B rows per workgroup tile (both variants)
@@ -269,9 +270,16 @@ struct Layout {
 };
 
 Layout layout_for(int64_t T, int H, int I, int E, int top_k, bool with_route) {
-    const Plan pl = plan_for(T, E, top_k);
+    // Every buffer sized for whichever tile height (reference or packed layout) needs more: the
+    // padded row count grows with block_m, the tile count shrinks with it.
     const int64_t numel = T * top_k;
-    const int64_t mp = max_padded_rows(numel, E, pl.block_m);
+    int64_t mp = 0, tiles = 0;
+    for (bool packed : {false, true}) {
+        const int bm = plan_for(T, E, top_k, packed).block_m;
+        const int64_t m = max_padded_rows(numel, E, bm);
+        mp = std::max(mp, m);
+        tiles = std::max(tiles, m / bm);
+    }
     Layout L{};
     size_t off = 0;
     auto take = [&](size_t bytes) {
@@ -280,7 +288,7 @@ Layout layout_for(int64_t T, int H, int I, int E, int top_k, bool with_route) {
         return at;
     };
     L.sorted = take(sizeof(int32_t) * mp);
-    L.expert_ids = take(sizeof(int32_t) * (mp / pl.block_m));
+    L.expert_ids = take(sizeof(int32_t) * tiles);
     L.total = take(sizeof(int32_t));
     L.hist = take(align_workspace_bytes(numel, E));
     L.act = take(sizeof(bf16_t) * mp * I);
@@ -318,12 +326,14 @@ GemmArgs gemm_args(const bf16_t* A, const bf16_t* B, bf16_t* C, const float* top
     g.top_k = top_k;
     g.N = N;
     g.K = K;
-    g.m_tiles = (int)(max_padded_rows(numel, E, block_m) / block_m);
+    g.m_tiles = (int)active_tile_bound(numel, E, block_m);
     g.n_tiles = n_tiles;
     return g;
 }
 
-bool block_m_supported(int block_m) { return block_m == 16 || block_m == 64; }
+bool block_m_supported(int block_m, bool packed) {
+    return block_m == 16 || block_m == 64 || (packed && block_m == 128);
+}
 
 // gate_up GEMM + SwiGLU: act[max_padded, I] from x[T, H] and w13[E, 2I, H].
 template <int BM, int WM, int WN, bool GATEUP>
@@ -343,6 +353,7 @@ void launch_gate_up(const bf16_t* x, const bf16_t* w13, const int32_t* sorted,
     GemmArgs g = gemm_args(x, w13, act, nullptr, sorted, eids, total, numel, top_k, I, H, E,
                            block_m, I / (kBN / 2));
     if (block_m == 16 && launch_stream_gate_up(g, packed, stream)) return;
+    if (packed && block_m >= 64 && launch_tile_gate_up(g, block_m, stream)) return;
     if (block_m == 16)
         launch_lds<16, 1, 4, true>(g, packed, stream);
     else
@@ -356,6 +367,7 @@ void launch_down(const bf16_t* act, const bf16_t* w2, const float* topk_w, const
     GemmArgs g = gemm_args(act, w2, rows, topk_w, sorted, eids, total, numel, 1, H, I, E,
                            block_m, H / kBN);
     if (block_m == 16 && launch_stream_down(g, packed, stream)) return;
+    if (packed && block_m >= 64 && launch_tile_down(g, block_m, stream)) return;
     if (block_m == 16)
         launch_lds<16, 1, 4, false>(g, packed, stream);
     else
@@ -373,8 +385,16 @@ void launch_combine(const bf16_t* rows, int64_t T, int H, int top_k, bf16_t* out
 int run_experts(const void* x, const void* w13, const void* w2, const float* topk_w,
                 const int32_t* topk_ids, int64_t T, int H, int I, int E, int top_k, int sum_topk,
                 bool packed, void* out, char* ws, const Layout& L, hipStream_t stream) {
-    const Plan pl = plan_for(T, E, top_k);
+    const Plan pl = plan_for(T, E, top_k, packed);
     const int64_t numel = T * top_k;
+    {   // the workspace regions must hold this plan's buffers (host-side guard, no launch if not)
+        const int64_t mp = max_padded_rows(numel, E, pl.block_m);
+        const bool fits = L.expert_ids - L.sorted >= sizeof(int32_t) * (size_t)mp &&
+                          L.total - L.expert_ids >= sizeof(int32_t) * (size_t)(mp / pl.block_m) &&
+                          L.rows - L.act >= sizeof(bf16_t) * (size_t)(mp * I);
+        TSM_REQUIRE(fits, TSM_E_WORKSPACE, "internal: workspace layout does not fit block_m %d",
+                    pl.block_m);
+    }
     int32_t* sorted = reinterpret_cast<int32_t*>(ws + L.sorted);
     int32_t* eids = reinterpret_cast<int32_t*>(ws + L.expert_ids);
     int32_t* total = reinterpret_cast<int32_t*>(ws + L.total);
@@ -395,10 +415,10 @@ int run_experts(const void* x, const void* w13, const void* w2, const float* top
 
 using namespace tsm;
 
-extern "C" int tsm_moe_block_m(int64_t T, int H, int I, int E, int top_k) {
+extern "C" int tsm_moe_block_m(int64_t T, int H, int I, int E, int top_k, int weight_layout) {
     (void)H;
     (void)I;
-    return plan_for(T, E, top_k).block_m;
+    return plan_for(T, E, top_k, weight_layout != 0).block_m;
 }
 
 extern "C" int tsm_silu_and_mul(const void* gate, int64_t gate_stride, const void* up,
@@ -515,8 +535,8 @@ extern "C" int tsm_moe_gemm_gate_up(const void* x, const void* w13, const int32_
     clear_error();
     int rc = check_moe_shapes(numel / (top_k > 0 ? top_k : 1), H, I, E, top_k);
     if (rc) return rc;
-    TSM_REQUIRE(block_m_supported(block_m), TSM_E_SHAPE, "block_m %d has no kernel (16 or 64)",
-                block_m);
+    TSM_REQUIRE(block_m_supported(block_m, weight_layout != 0), TSM_E_SHAPE,
+                "block_m %d has no kernel for this weight layout", block_m);
     if (numel == 0) return TSM_OK;
     TSM_REQUIRE(x && w13 && sorted_ids && expert_ids && total && act, TSM_E_ARG,
                 "null pointer argument");
@@ -533,8 +553,8 @@ extern "C" int tsm_moe_gemm_down(const void* act, const void* w2, const float* t
     clear_error();
     int rc = check_moe_shapes(numel, H, I, E, 1);
     if (rc) return rc;
-    TSM_REQUIRE(block_m_supported(block_m), TSM_E_SHAPE, "block_m %d has no kernel (16 or 64)",
-                block_m);
+    TSM_REQUIRE(block_m_supported(block_m, weight_layout != 0), TSM_E_SHAPE,
+                "block_m %d has no kernel for this weight layout", block_m);
     if (numel == 0) return TSM_OK;
     TSM_REQUIRE(act && w2 && topk_w && sorted_ids && expert_ids && total && rows, TSM_E_ARG,
                 "null pointer argument");

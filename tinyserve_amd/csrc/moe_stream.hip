@@ -28,13 +28,16 @@ __device__ __forceinline__ float swiglu_ref(float g, float u) {
     return s * u;
 }
 
-// S: MFMA k-steps per wavefront (K = 4 * 32 * S). NB: 16-row B blocks per workgroup; for gate_up
-// NB = 2 (one gate block and the matching up block -> 16 activation columns).
-template <int S, int NB, bool GATEUP, bool PACKED>
-__global__ __launch_bounds__(256, 2) void moe_stream_kernel(GemmArgs p) {
+// S: MFMA k-steps per wavefront (K = 4 * 32 * S). NB: 16-row B blocks per wavefront; for gate_up
+// NB = 2 (one gate block and the matching up block -> 16 activation columns). WN: groups of 4
+// wavefronts, each group taking the next NB blocks (down GEMM only).
+template <int S, int NB, int WN, bool GATEUP, bool PACKED>
+__global__ __launch_bounds__(256 * WN, 2 / WN) void moe_stream_kernel(GemmArgs p) {
+    static_assert(!GATEUP || WN == 1, "gate_up uses one wavefront group");
     constexpr int BM = 16;
-    constexpr int OUTC = GATEUP ? 16 : 16 * NB;  // output columns per workgroup
-    __shared__ f32x4 red[4][NB][64];
+    constexpr int NT = 256 * WN;                      // threads
+    constexpr int OUTC = GATEUP ? 16 : 16 * NB * WN;  // output columns per workgroup
+    __shared__ f32x4 red[4][WN * NB][64];
 
     const int G = p.m_tiles * p.n_tiles;
     const int pid = blockIdx.x;
@@ -44,11 +47,11 @@ __global__ __launch_bounds__(256, 2) void moe_stream_kernel(GemmArgs p) {
     const int m0 = m_tile * BM;
     if (m0 >= p.total[0]) return;
     const int expert = p.expert_ids[m_tile];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = (tid >> 6) & 3, wgrp = tid >> 8;
 
     if (expert < 0) {
         if (!GATEUP) {
-            for (int idx = tid; idx < BM * (OUTC / 8); idx += 256) {
+            for (int idx = tid; idx < BM * (OUTC / 8); idx += NT) {
                 const int row = idx / (OUTC / 8), cc = idx % (OUTC / 8);
                 const int flat = p.sorted_ids[m0 + row];
                 if (flat < p.numel)
@@ -69,13 +72,13 @@ __global__ __launch_bounds__(256, 2) void moe_stream_kernel(GemmArgs p) {
         const u32x4* src;
         int stride;  // in 16-byte units between consecutive k-steps
         if (PACKED) {
-            const int blk = GATEUP ? 2 * n_tile + nb : n_tile * NB + nb;
+            const int blk = GATEUP ? 2 * n_tile + nb : (n_tile * WN + wgrp) * NB + nb;
             src = reinterpret_cast<const u32x4*>(
                       Be + ((int64_t)blk * (p.K / 32) + wave * S) * 512) + lane;
             stride = 64;
         } else {
             const int row = GATEUP ? (nb == 0 ? 0 : p.N) + n_tile * 16 + r
-                                   : n_tile * OUTC + nb * 16 + r;
+                                   : n_tile * OUTC + (wgrp * NB + nb) * 16 + r;
             src = reinterpret_cast<const u32x4*>(Be + (int64_t)row * p.K + kbase);
             stride = 4;
         }
@@ -109,16 +112,19 @@ __global__ __launch_bounds__(256, 2) void moe_stream_kernel(GemmArgs p) {
             acc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a[s]), as_bf16x8(b[nb][s]),
                                                               acc[nb], 0, 0, 0);
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) red[wave][nb][lane] = acc[nb];
+    for (int nb = 0; nb < NB; ++nb) red[wave][wgrp * NB + nb][lane] = acc[nb];
     __syncthreads();
 
-    // Thread (lane l, element i) finalises row (l/16)*4 + i, column l%16 of every block.
-    const int l = tid & 63, i = tid >> 6;
+    // Thread (lane l, element i, group g) finalises row (l/16)*4 + i, column l%16 of the blocks
+    // of group g, summing the four K-quarter partials in fixed order.
+    const int l = tid & 63, i = (tid >> 6) & 3;
     const int row = (l >> 4) * 4 + i, col = l & 15;
     float v[NB];
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb)
-        v[nb] = ((red[0][nb][l][i] + red[1][nb][l][i]) + red[2][nb][l][i]) + red[3][nb][l][i];
+    for (int nb = 0; nb < NB; ++nb) {
+        const int bb = wgrp * NB + nb;
+        v[nb] = ((red[0][bb][l][i] + red[1][bb][l][i]) + red[2][bb][l][i]) + red[3][bb][l][i];
+    }
     if (GATEUP) {
         p.C[(int64_t)(m0 + row) * p.N + n_tile * 16 + col] = f32_to_bf16(swiglu_ref(v[0], v[1]));
     } else {
@@ -127,15 +133,16 @@ __global__ __launch_bounds__(256, 2) void moe_stream_kernel(GemmArgs p) {
             const float w = p.topk_w[flat];
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb)
-                p.C[(int64_t)flat * p.N + n_tile * OUTC + nb * 16 + col] = f32_to_bf16(v[nb] * w);
+                p.C[(int64_t)flat * p.N + n_tile * OUTC + (wgrp * NB + nb) * 16 + col] =
+                    f32_to_bf16(v[nb] * w);
         }
     }
 }
 
-template <int S, int NB, bool GATEUP, bool PACKED>
+template <int S, int NB, bool GATEUP, bool PACKED, int WN = 1>
 void launch_s(const GemmArgs& g, hipStream_t stream) {
-    hipLaunchKernelGGL((moe_stream_kernel<S, NB, GATEUP, PACKED>), dim3(g.m_tiles * g.n_tiles),
-                       dim3(256), 0, stream, g);
+    hipLaunchKernelGGL((moe_stream_kernel<S, NB, WN, GATEUP, PACKED>),
+                       dim3(g.m_tiles * g.n_tiles), dim3(256 * WN), 0, stream, g);
 }
 
 template <bool PACKED>
@@ -151,18 +158,18 @@ bool gate_up_s(const GemmArgs& g, hipStream_t stream) {
     }
 }
 
-// Down GEMM: four 16-column blocks per workgroup when the K slice is short (register budget),
-// two otherwise.
+// Down GEMM: two groups of four wavefronts, four 16-column blocks each (128 columns per
+// workgroup) when the K slice is short (register budget); two blocks, one group otherwise.
 template <bool PACKED>
 bool down_s(GemmArgs g, hipStream_t stream) {
     const int S = g.K / 128;
-    if (S <= 8 && g.N % 64 == 0) {
-        g.n_tiles = g.N / 64;
+    if (S <= 8 && g.N % 128 == 0) {
+        g.n_tiles = g.N / 128;
         switch (S) {
-            case 2: launch_s<2, 4, false, PACKED>(g, stream); return true;
-            case 4: launch_s<4, 4, false, PACKED>(g, stream); return true;
-            case 6: launch_s<6, 4, false, PACKED>(g, stream); return true;
-            case 8: launch_s<8, 4, false, PACKED>(g, stream); return true;
+            case 2: launch_s<2, 4, false, PACKED, 2>(g, stream); return true;
+            case 4: launch_s<4, 4, false, PACKED, 2>(g, stream); return true;
+            case 6: launch_s<6, 4, false, PACKED, 2>(g, stream); return true;
+            case 8: launch_s<8, 4, false, PACKED, 2>(g, stream); return true;
             default: return false;
         }
     }

@@ -39,9 +39,10 @@ def fused_moe(x, w13, w2, topk_weights, topk_ids, sum_topk=True):
     return ops.fused_moe(x, w13, w2, topk_weights, topk_ids, sum_topk)
 
 
-def moe_block_m(T: int, H: int, I: int, E: int, top_k: int) -> int:
-    """Tile height fused_moe uses for T tokens (its own table, not the reference's rule)."""
-    return int(lib.tsm_moe_block_m(T, H, I, E, top_k))
+def moe_block_m(T: int, H: int, I: int, E: int, top_k: int, packed: bool = False) -> int:
+    """Tile height fused_moe (packed=False) or fused_moe_packed (packed=True) uses for T tokens
+    (its own table, not the reference's rule)."""
+    return int(lib.tsm_moe_block_m(T, H, I, E, top_k, int(packed)))
 
 
 @torch.inference_mode()
