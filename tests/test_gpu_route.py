@@ -74,8 +74,8 @@ def test_router_fused_bitexact(dev, tsm, qwen_layer, T, logits_bf16):
                                          (1024, 60, 4, torch.bfloat16), (4096, 16, 4,
                                                                          torch.float32),
                                          (136, 5, 3, torch.float32)])
-def test_router_fused_shapes(dev, tsm, H, E, k, dtype):
-    T = 37
+@pytest.mark.parametrize("T", [37, 300])
+def test_router_fused_shapes(dev, tsm, H, E, k, dtype, T):
     g = torch.Generator().manual_seed(H + E)
     x = torch.randn(T, H, generator=g).to(dtype)
     gw = (torch.randn(E, H, generator=g) * 0.05).to(dtype)

@@ -218,6 +218,122 @@ __global__ __launch_bounds__(kRouterWaves * 64) void router_kernel(
     }
 }
 
+// Large batches: the same logits (identical per-lane fma chains, identical addition tree) computed
+// for a tile of 8 tokens x 8 experts per wavefront. Lane j accumulates its 32-element partial for
+// all 64 (token, expert) pairs; the 64 x 64 partials are then combined by a transposed
+// reduce-scatter (at distance s = 32, 16, ..., 1 each lane keeps half of its pairs and adds the
+// partner's values for them), which pairs lanes exactly as wave_sum_butterfly does, so every sum
+// is bit-identical to the per-pair butterfly while costing about two shuffles per pair instead of
+// six. The 8 tokens' x rows are staged in LDS; each gate row streamed from L2 serves 8 tokens.
+constexpr int kTT = 8;   // tokens per workgroup
+constexpr int kEG = 8;   // experts per wavefront group
+constexpr int kTileWaves = 8;
+
+template <typename TIn, int NC>
+__global__ __launch_bounds__(kTileWaves * 64) void router_tile_kernel(
+    const TIn* __restrict__ x, const TIn* __restrict__ gw, int64_t T, int H, int E, int top_k,
+    int renorm, const int64_t* __restrict__ expert_map, const float* __restrict__ bias,
+    int logits_bf16, float* __restrict__ logits_out, float* __restrict__ topk_w,
+    int32_t* __restrict__ topk_ids) {
+#pragma clang fp contract(off)
+    constexpr int W = NC * 512;
+    constexpr int EPC = 16 / sizeof(TIn);
+    __shared__ __attribute__((aligned(16))) TIn s_x[kTT * W];
+    __shared__ float s_logits[kTT * 512];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int64_t t0 = (int64_t)blockIdx.x * kTT;
+
+    for (int idx = threadIdx.x; idx < kTT * W / EPC; idx += kTileWaves * 64) {
+        const int tb = idx / (W / EPC), h = (idx % (W / EPC)) * EPC;
+        u32x4 v = u32x4{0u, 0u, 0u, 0u};
+        if (t0 + tb < T && h < H) v = *reinterpret_cast<const u32x4*>(x + (t0 + tb) * H + h);
+        *reinterpret_cast<u32x4*>(s_x + tb * W + h) = v;
+    }
+    __syncthreads();
+
+    const int groups = (E + kEG - 1) / kEG;
+    for (int grp = wave; grp < groups; grp += kTileWaves) {
+        float acc[kTT * kEG];  // pair p = tt * kEG + ee
+#pragma unroll
+        for (int pi = 0; pi < kTT * kEG; ++pi) acc[pi] = 0.0f;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            const int h0 = c * 512 + lane * 8;
+            if (h0 < H) {
+                float g[kEG][8];
+#pragma unroll
+                for (int ee = 0; ee < kEG; ++ee) {
+                    const int e = grp * kEG + ee;
+                    Chunk8<TIn> ch;
+                    ch.zero();
+                    if (e < E) ch.load(gw + (int64_t)e * H + h0);
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) g[ee][i] = ch.get(i);
+                }
+#pragma unroll
+                for (int tt = 0; tt < kTT; ++tt) {
+                    Chunk8<TIn> xc;
+                    xc.load(s_x + tt * W + h0);
+                    float xv[8];
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) xv[i] = xc.get(i);
+#pragma unroll
+                    for (int ee = 0; ee < kEG; ++ee)
+#pragma unroll
+                        for (int i = 0; i < 8; ++i)
+                            acc[tt * kEG + ee] = __builtin_fmaf(xv[i], g[ee][i], acc[tt * kEG + ee]);
+                }
+            }
+        }
+        // transposed reduce-scatter: after the step at distance s, lane l holds the pairs whose
+        // index bits above log2(s) match its own; the last lane holding pair p is l == p.
+#pragma unroll
+        for (int s = 32, n = 64; s >= 1; s >>= 1, n >>= 1) {
+            const bool upper = (lane & s) != 0;
+#pragma unroll
+            for (int k = 0; k < n / 2; ++k) {
+                const float send = upper ? acc[k] : acc[k + n / 2];
+                const float keep = upper ? acc[k + n / 2] : acc[k];
+                acc[k] = keep + __shfl_xor(send, s);
+            }
+        }
+        const int tt = lane / kEG, e = grp * kEG + lane % kEG;
+        if (e < E) {
+            float l = acc[0];
+            if (bias) l = l + bias[e];
+            if (logits_bf16) l = round_bf16(l);
+            s_logits[tt * E + e] = l;
+            if (logits_out && t0 + tt < T) logits_out[(t0 + tt) * E + e] = l;
+        }
+    }
+    __syncthreads();
+
+    for (int tb = wave; tb < kTT; tb += kTileWaves) {
+        const int64_t t = t0 + tb;
+        if (t >= T) break;
+        float v[kMaxM];
+#pragma unroll
+        for (int q = 0; q < kMaxM; ++q) {
+            int e = lane + 64 * q;
+            v[q] = e < E ? s_logits[tb * E + e] : 0.0f;
+        }
+        wave_select(v, E, top_k, renorm, expert_map, topk_w + t * top_k, topk_ids + t * top_k);
+    }
+}
+
+template <typename TIn, int NC>
+hipError_t launch_router_tile(const void* x, const void* gw, int64_t T, int H, int E, int top_k,
+                              int renorm, const int64_t* expert_map, const float* bias,
+                              int logits_bf16, float* logits_out, float* w, int32_t* ids,
+                              hipStream_t stream) {
+    const int64_t blocks = (T + kTT - 1) / kTT;
+    hipLaunchKernelGGL((router_tile_kernel<TIn, NC>), dim3((unsigned)blocks),
+                       dim3(kTileWaves * 64), 0, stream, (const TIn*)x, (const TIn*)gw, T, H, E,
+                       top_k, renorm, expert_map, bias, logits_bf16, logits_out, w, ids);
+    return hipGetLastError();
+}
+
 template <typename TIn, int NC, int TB>
 hipError_t launch_router_tb(const void* x, const void* gw, int64_t T, int H, int E, int top_k,
                             int renorm, const int64_t* expert_map, const float* bias,
@@ -231,19 +347,18 @@ hipError_t launch_router_tb(const void* x, const void* gw, int64_t T, int H, int
     return hipGetLastError();
 }
 
-// Tokens per workgroup: one for decode-sized batches (more workgroups, lower latency); for larger
-// batches as many as keep the x slice within 64 fp32 registers per lane.
+// Decode-sized batches: one token per workgroup, x in registers (more workgroups, lower latency).
+// Larger batches: 8-token tiles with the transposed reduction.
 template <typename TIn, int NC>
 hipError_t launch_router_nc(const void* x, const void* gw, int64_t T, int H, int E, int top_k,
                             int renorm, const int64_t* expert_map, const float* bias,
                             int logits_bf16, float* logits_out, float* w, int32_t* ids,
                             hipStream_t stream) {
-    constexpr int TBMAX = (8 / NC) > 0 ? (8 / NC) : 1;
-    if (T <= 256 || TBMAX == 1)
+    if (T <= 256)
         return launch_router_tb<TIn, NC, 1>(x, gw, T, H, E, top_k, renorm, expert_map, bias,
                                             logits_bf16, logits_out, w, ids, stream);
-    return launch_router_tb<TIn, NC, TBMAX>(x, gw, T, H, E, top_k, renorm, expert_map, bias,
-                                            logits_bf16, logits_out, w, ids, stream);
+    return launch_router_tile<TIn, NC>(x, gw, T, H, E, top_k, renorm, expert_map, bias,
+                                       logits_bf16, logits_out, w, ids, stream);
 }
 
 template <typename TIn>

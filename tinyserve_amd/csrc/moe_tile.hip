@@ -40,34 +40,39 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-// LDS reads as inline assembly: the compiler's wait-count pass cannot see that the ring slot
-// being read is not the one the in-flight global->LDS loads target and would otherwise drain all
-// loads before every read. Completion is tracked by hand (wait_vmcnt before the barrier that
-// publishes a stage; lgkmcnt(0) before the MFMAs that consume a read).
+// The compiler does not order LDS reads after the global->LDS loads that fill them, and
+// __syncthreads() would drain every outstanding load (a release fence) before each barrier. The
+// ring is therefore synchronised by hand: each wavefront waits (vmcnt) for its own loads of the
+// stage it is about to read and for its own LDS reads of the previous stage (lgkmcnt), then a
+// plain s_barrier publishes the stage to every wavefront and frees the slot the next loads
+// overwrite. The asm statements carry "memory" clobbers so no LDS access moves across them.
 __device__ __forceinline__ u32x4 lds_read16(uint32_t addr) {
-    u32x4 v;
-    asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr) : "memory");
-    return v;
+    return *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(addr);
 }
-__device__ __forceinline__ void wait_lgkm0() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
-__device__ __forceinline__ void barrier_nofence() { asm volatile("s_barrier" ::: "memory"); }
+__device__ __forceinline__ void barrier_after_lds_reads() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
 
-constexpr int kStageK = 2;   // MFMA k-steps (of 32) per pipeline stage
-constexpr int kStages = 3;   // LDS ring depth
 constexpr int kBN = 256;     // B rows per tile
 constexpr int kBlk = 1024;   // bytes per 16x32 operand block
 
-template <int BM, bool GATEUP>
-__global__ __launch_bounds__(256, 1) void moe_tile_kernel(GemmArgs p) {
+
+// kStageK: MFMA k-steps (of 32) per pipeline stage; kStages: LDS ring depth (kStages - 1 stages
+// of loads in flight while one is consumed); NW: wavefronts (2 x NW/2 grid over the tile).
+template <int BM, bool GATEUP, int kStageK, int kStages, int NW>
+__global__ __launch_bounds__(64 * NW, 2) void moe_tile_kernel(GemmArgs p) {
+    constexpr int NT = 64 * NW;
+    constexpr int WN = NW / 2;              // wavefront columns
     constexpr int MB = BM / 16;             // A row blocks per tile
     constexpr int NBK = kBN / 16;           // B row blocks per tile (16)
     constexpr int A_BLKS = MB * kStageK;    // A blocks per stage
     constexpr int B_BLKS = NBK * kStageK;   // B blocks per stage
-    constexpr int STAGE_BYTES = (A_BLKS + B_BLKS) * kBlk;
-    constexpr int A_PER_WAVE = A_BLKS / 4, B_PER_WAVE = B_BLKS / 4;
+    constexpr int NBLK = A_BLKS + B_BLKS;
+    constexpr int STAGE_BYTES = NBLK * kBlk;
+    constexpr int LPW = (NBLK + NW - 1) / NW;  // load slots per wavefront per stage
     constexpr int FM = MB / 2;              // A blocks per wavefront (rows BM/2)
-    constexpr int FN = NBK / 2;             // B blocks per wavefront (8)
-    static_assert(A_BLKS % 4 == 0 && B_BLKS % 4 == 0, "even split of loads over wavefronts");
+    constexpr int FN = NBK / WN;            // B blocks per wavefront
+    static_assert(!GATEUP || FN % 2 == 0, "gate/up block pairs per wavefront");
     extern __shared__ __attribute__((aligned(1024))) char lds[];
 
     const int G = p.m_tiles * p.n_tiles;
@@ -83,7 +88,7 @@ __global__ __launch_bounds__(256, 1) void moe_tile_kernel(GemmArgs p) {
 
     if (expert < 0) {
         if (!GATEUP) {
-            for (int idx = tid; idx < BM * (OUTC / 8); idx += 256) {
+            for (int idx = tid; idx < BM * (OUTC / 8); idx += NT) {
                 const int row = idx / (OUTC / 8), cc = idx % (OUTC / 8);
                 const int flat = p.sorted_ids[m0 + row];
                 if (flat < p.numel)
@@ -98,51 +103,49 @@ __global__ __launch_bounds__(256, 1) void moe_tile_kernel(GemmArgs p) {
     const int KS = p.K / 32;                 // k-steps
     const int NST = KS / kStageK;            // stages
 
-    // Per-lane global sources. A: this wavefront loads row blocks mb = wave*A_PER_WAVE/kStageK..
-    // (each for kStageK k-steps); the lane's row and 16-byte column inside the 16x32 block.
-    constexpr int AMB = A_PER_WAVE / kStageK;  // A row blocks loaded per wavefront
-    const bf16_t* a_row[AMB > 0 ? AMB : 1];
+    // Load slots: wavefront w loads blocks w, w + NW, ... of every stage (A blocks first, then B),
+    // each lane the 16 bytes it will read back from LDS. A block (row block mb, k-step kk): the
+    // lane's gathered row at column 32*kk + 8*q; B block: 16-row block nb of the packed weights.
+    const bf16_t* src[LPW];
+    int stride[LPW];   // elements per stage
 #pragma unroll
-    for (int j = 0; j < AMB; ++j) {
-        const int row = m0 + (wave * AMB + j) * 16 + r;
-        int64_t src_row;
-        if (GATEUP) {
-            int flat = p.sorted_ids[row];
-            if (flat >= p.numel) flat = 0;  // padding row: any valid row, result discarded
-            src_row = flat / p.top_k;
-        } else {
-            src_row = row;
+    for (int j = 0; j < LPW; ++j) {
+        const int b = wave + j * NW;
+        src[j] = nullptr;
+        stride[j] = 0;
+        if (b < A_BLKS) {
+            const int mb = b / kStageK, kk = b % kStageK;
+            const int row = m0 + mb * 16 + r;
+            int64_t src_row;
+            if (GATEUP) {
+                int flat = p.sorted_ids[row];
+                if (flat >= p.numel) flat = 0;  // padding row: any valid row, result discarded
+                src_row = flat / p.top_k;
+            } else {
+                src_row = row;
+            }
+            src[j] = p.A + src_row * p.K + kk * 32 + q * 8;
+            stride[j] = kStageK * 32;
+        } else if (b < NBLK) {
+            const int nb = (b - A_BLKS) / kStageK, kk = (b - A_BLKS) % kStageK;
+            const bf16_t* Be = p.B + (int64_t)expert * (GATEUP ? 2 : 1) * p.N * p.K;
+            src[j] = Be + ((int64_t)(n_tile * NBK + nb) * KS + kk) * 512 + lane * 8;
+            stride[j] = kStageK * 512;
         }
-        a_row[j] = p.A + src_row * p.K + q * 8;
     }
-    // B: this wavefront loads n-blocks wave*BNB.. of the tile, all kStageK k-steps.
-    constexpr int BNB = B_PER_WAVE / kStageK;
-    const bf16_t* Be = p.B + (int64_t)expert * (GATEUP ? 2 : 1) * p.N * p.K;
-    const bf16_t* b_blk = Be + ((int64_t)(n_tile * NBK + wave * BNB) * KS) * 512 + lane * 8;
-
     auto issue = [&](int st) {
         char* base = lds + (st % kStages) * STAGE_BYTES;
 #pragma unroll
-        for (int j = 0; j < AMB; ++j)
-#pragma unroll
-            for (int kk = 0; kk < kStageK; ++kk) {
-                const int blk = (wave * AMB + j) * kStageK + kk;
-                __builtin_amdgcn_global_load_lds(
-                    (const void*)(a_row[j] + (st * kStageK + kk) * 32),
-                    (lds_void*)(base + blk * kBlk), 16, 0, 0);
-            }
-#pragma unroll
-        for (int j = 0; j < BNB; ++j)
-#pragma unroll
-            for (int kk = 0; kk < kStageK; ++kk) {
-                const int blk = A_BLKS + (wave * BNB + j) * kStageK + kk;
-                __builtin_amdgcn_global_load_lds(
-                    (const void*)(b_blk + ((int64_t)j * KS + st * kStageK + kk) * 512),
-                    (lds_void*)(base + blk * kBlk), 16, 0, 0);
-            }
+        for (int j = 0; j < LPW; ++j) {
+            const int b = wave + j * NW;
+            if (NBLK % NW == 0 || b < NBLK)
+                __builtin_amdgcn_global_load_lds((const void*)(src[j] + (int64_t)st * stride[j]),
+                                                 (lds_void*)(base + b * kBlk), 16, 0, 0);
+        }
     };
+    // LDS slot of A block (mb, kk): mb*kStageK + kk; of B block (nb, kk): A_BLKS + nb*kStageK+kk
 
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave / WN, wn = wave % WN;
     f32x4 acc[FM][FN];
 #pragma unroll
     for (int f = 0; f < FM; ++f)
@@ -169,25 +172,31 @@ __global__ __launch_bounds__(256, 1) void moe_tile_kernel(GemmArgs p) {
                     as_bf16x8(af[f]), as_bf16x8(bfr[g]), acc[f][g], 0, 0, 0);
     };
 
-    issue(0);
-    if (NST > 1) issue(1);
+    // Loads issued per wavefront per stage (slots beyond NBLK issue nothing).
+    constexpr int LPS = (NBLK % NW == 0) ? LPW : -1;
+    static_assert(LPS > 0, "stage blocks must split evenly over the wavefronts");
+    constexpr int NPRE = kStages - 1;              // stages in flight ahead of the one read
+#pragma unroll
+    for (int st = 0; st < NPRE; ++st)
+        if (st < NST) issue(st);
     for (int st = 0; st < NST; ++st) {
-        // this wavefront's loads for stage st are done once at most one later stage is pending;
-        // the barrier then publishes every wavefront's share and retires the reads of st - 1
-        if (st + 1 < NST)
-            wait_vmcnt<A_PER_WAVE + B_PER_WAVE>();
-        else
-            wait_vmcnt<0>();
-        barrier_nofence();
-        if (st + 2 < NST) issue(st + 2);
-        static_assert(kStageK == 2, "two k-steps per stage");
-        u32x4 a0[FM], b0[FN], a1[FM], b1[FN];
-        read_frags(st, 0, a0, b0);
-        wait_lgkm0();
-        read_frags(st, 1, a1, b1);
-        mfmas(a0, b0);
-        wait_lgkm0();
-        mfmas(a1, b1);
+        // this wavefront's loads for stage st are done once only the later stages it has issued
+        // are pending; the barrier then publishes every wavefront's share of stage st and
+        // retires the reads of st - 1, whose slot the next issue overwrites
+        const int later = min(NPRE - 1, NST - 1 - st);
+        if (later >= NPRE - 1) wait_vmcnt<LPS * (NPRE - 1)>();
+        else if (NPRE >= 3 && later == 1) wait_vmcnt<LPS>();
+        else if (NPRE >= 4 && later == 2) wait_vmcnt<(NPRE >= 4 ? LPS * 2 : 0)>();
+        else if (NPRE >= 5 && later == 3) wait_vmcnt<(NPRE >= 5 ? LPS * 3 : 0)>();
+        else wait_vmcnt<0>();
+        barrier_after_lds_reads();
+        if (st + NPRE < NST) issue(st + NPRE);
+#pragma unroll
+        for (int kk = 0; kk < kStageK; ++kk) {
+            u32x4 af[FM], bfr[FN];
+            read_frags(st, kk, af, bfr);
+            mfmas(af, bfr);
+        }
     }
 
     // Epilogue: element i of block (f, g) is row (lane/16)*4 + i, column lane%16.
@@ -221,16 +230,19 @@ __global__ __launch_bounds__(256, 1) void moe_tile_kernel(GemmArgs p) {
 
 template <int BM, bool GATEUP>
 void launch_tile(GemmArgs g, hipStream_t stream) {
-    constexpr int stage = (BM / 16 + kBN / 16) * kStageK * kBlk;
-    const size_t lds = (size_t)kStages * stage;
+    constexpr int NW = BM >= 128 ? 8 : 4;                       // wavefronts per workgroup
+    constexpr int SK = ((BM / 16 + kBN / 16) % NW == 0) ? 1 : 2;  // k-steps per stage
+    constexpr int stage = (BM / 16 + kBN / 16) * SK * kBlk;     // bytes per stage
+    constexpr int NS = (80 * 1024) / stage > 6 ? 6 : (80 * 1024) / stage;  // ring depth, 2 WG/CU
+    const size_t lds = (size_t)NS * stage;
     static bool configured = false;
     if (!configured) {
-        (void)hipFuncSetAttribute((const void*)moe_tile_kernel<BM, GATEUP>,
+        (void)hipFuncSetAttribute((const void*)moe_tile_kernel<BM, GATEUP, SK, NS, NW>,
                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         configured = true;
     }
-    hipLaunchKernelGGL((moe_tile_kernel<BM, GATEUP>), dim3(g.m_tiles * g.n_tiles), dim3(256), lds,
-                       stream, g);
+    hipLaunchKernelGGL((moe_tile_kernel<BM, GATEUP, SK, NS, NW>), dim3(g.m_tiles * g.n_tiles),
+                       dim3(64 * NW), lds, stream, g);
 }
 
 }  // namespace
