@@ -62,6 +62,11 @@ def main():
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a plain 1 GiB device copy (counter calibration for rocprofv3)")
+    ap.add_argument("--traffic-json", default=os.path.join(
+        os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic_gate_up_T64.json"),
+                    help="HBM traffic per gate_up launch measured with rocprofv3 --pmc")
     ap.add_argument("--profile", action="store_true",
                     help="eager stage launches only (for rocprofv3 runs); no sweep, no CPU leg")
     args = ap.parse_args()
@@ -71,6 +76,15 @@ def main():
         sys.exit(2)
 
     import torch
+    if args.copy_calibration:
+        n = 1 << 30
+        src = torch.empty(n, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": n}), flush=True)
+        return
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     lib_path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "tinyserve_amd",
                             "libtinyserve_moe.so")
@@ -141,61 +155,83 @@ def main():
         return ms, sum(touched) / len(touched)
 
     def time_stages(T, steps, warmup):
-        """Eager launches of each stage through the C ABI with HIP events between stages on the
-        launch stream. Returns mean ms per stage launch."""
+        """Per-stage kernel times: every stage is launched `steps` times back to back through the
+        C ABI (cycling the layer copies, each with its own routing, permutation and
+        intermediates), captured in one HIP graph whose replay is bracketed by a pair of HIP
+        events on the replay stream. Returns mean ms per launch of each stage and the tile
+        height."""
         xs = inputs(T, 1000 + T)
         numel = T * K_TOP
         bm = int(lib.tsm_moe_block_m(T, H, I, E, K_TOP, 1))
         mp = int(lib.tsm_moe_max_padded(numel, E, bm))
-        w = torch.empty(T, K_TOP, dtype=torch.float32, device=dev)
-        ids = torch.empty(T, K_TOP, dtype=torch.int32, device=dev)
-        sorted_ids = torch.empty(mp, dtype=torch.int32, device=dev)
-        eids = torch.empty(mp // bm, dtype=torch.int32, device=dev)
-        total = torch.empty(1, dtype=torch.int32, device=dev)
         nws = int(lib.tsm_moe_align_workspace_size(numel, E, bm))
-        aws = torch.empty(max(nws, 1), dtype=torch.uint8, device=dev)
-        act = torch.empty(mp, I, dtype=torch.bfloat16, device=dev)
-        rows = torch.empty(numel, H, dtype=torch.bfloat16, device=dev)
-        out = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
-        stream = torch.cuda.current_stream()
-        sp = stream.cuda_stream
-        names = ["router", "align", "gate_up", "down", "combine"]
-        acc = {n: 0.0 for n in names}
+        st = []
+        for i in range(L):
+            st.append(dict(
+                w=torch.empty(T, K_TOP, dtype=torch.float32, device=dev),
+                ids=torch.empty(T, K_TOP, dtype=torch.int32, device=dev),
+                sorted_ids=torch.empty(mp, dtype=torch.int32, device=dev),
+                eids=torch.empty(mp // bm, dtype=torch.int32, device=dev),
+                total=torch.empty(1, dtype=torch.int32, device=dev),
+                aws=torch.empty(max(nws, 1), dtype=torch.uint8, device=dev),
+                act=torch.empty(mp, I, dtype=torch.bfloat16, device=dev),
+                rows=torch.empty(numel, H, dtype=torch.bfloat16, device=dev),
+                out=torch.empty(T, H, dtype=torch.bfloat16, device=dev)))
+        def cur():
+            return torch.cuda.current_stream().cuda_stream
 
-        def one(i, evs):
-            gw = layers[i % L][0]
-            w13, w2 = packed[i % L]
-            x = xs[i % L]
-            if evs: evs[0].record(stream)
-            check(lib.tsm_moe_router(ptr(x), ptr(gw), 1, T, H, E, K_TOP, 1, None, None, 0, None,
-                                     ptr(w), ptr(ids), sp), "router")
-            if evs: evs[1].record(stream)
-            check(lib.tsm_moe_align(ptr(ids), numel, E, bm, ptr(sorted_ids), ptr(eids),
-                                    ptr(total), ptr(aws), nws, sp), "align")
-            if evs: evs[2].record(stream)
-            check(lib.tsm_moe_gemm_gate_up(ptr(x), ptr(w13), ptr(sorted_ids), ptr(eids),
-                                           ptr(total), numel, K_TOP, H, I, E, bm, 1, ptr(act), sp),
-                  "gate_up")
-            if evs: evs[3].record(stream)
-            check(lib.tsm_moe_gemm_down(ptr(act), ptr(w2), ptr(w), ptr(sorted_ids), ptr(eids),
-                                        ptr(total), numel, H, I, E, bm, 1, ptr(rows), sp), "down")
-            if evs: evs[4].record(stream)
-            check(lib.tsm_moe_combine(ptr(rows), T, H, K_TOP, ptr(out), sp), "combine")
-            if evs: evs[5].record(stream)
+        def router(i):
+            c = st[i]
+            check(lib.tsm_moe_router(ptr(xs[i]), ptr(layers[i][0]), 1, T, H, E, K_TOP, 1, None,
+                                     None, 0, None, ptr(c["w"]), ptr(c["ids"]), cur()), "router")
 
-        for j in range(warmup):
-            one(j, None)
+        def align(i):
+            c = st[i]
+            check(lib.tsm_moe_align(ptr(c["ids"]), numel, E, bm, ptr(c["sorted_ids"]),
+                                    ptr(c["eids"]), ptr(c["total"]), ptr(c["aws"]), nws, cur()),
+                  "align")
+
+        def gate_up(i):
+            c = st[i]
+            check(lib.tsm_moe_gemm_gate_up(ptr(xs[i]), ptr(packed[i][0]), ptr(c["sorted_ids"]),
+                                           ptr(c["eids"]), ptr(c["total"]), numel, K_TOP, H, I,
+                                           E, bm, 1, ptr(c["act"]), cur()), "gate_up")
+
+        def down(i):
+            c = st[i]
+            check(lib.tsm_moe_gemm_down(ptr(c["act"]), ptr(packed[i][1]), ptr(c["w"]),
+                                        ptr(c["sorted_ids"]), ptr(c["eids"]), ptr(c["total"]),
+                                        numel, H, I, E, bm, 1, ptr(c["rows"]), cur()), "down")
+
+        def combine(i):
+            c = st[i]
+            check(lib.tsm_moe_combine(ptr(c["rows"]), T, H, K_TOP, ptr(c["out"]), cur()),
+                  "combine")
+
+        stages = [("router", router), ("align", align), ("gate_up", gate_up), ("down", down),
+                  ("combine", combine)]
+        for i in range(L):
+            for _, fn in stages:
+                fn(i)
         torch.cuda.synchronize()
-        all_evs = []
-        for j in range(steps):
-            evs = [torch.cuda.Event(enable_timing=True) for _ in range(6)]
-            one(j, evs)
-            all_evs.append(evs)
-        torch.cuda.synchronize()
-        for evs in all_evs:
-            for k, n in enumerate(names):
-                acc[n] += evs[k].elapsed_time(evs[k + 1])
-        return {n: acc[n] / steps for n in names}, bm
+        res = {}
+        for name, fn in stages:
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr):
+                for j in range(steps):
+                    fn(j % L)
+            for _ in range(max(1, warmup // max(steps, 1))):
+                gr.replay()
+            torch.cuda.synchronize()
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record()
+            gr.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            res[name] = e0.elapsed_time(e1) / steps
+            del gr
+        return res, bm
 
     T = args.tokens
     log(f"stage timing T={T}")
@@ -221,11 +257,20 @@ def main():
         "peak": HBM_PEAK / 1e9,
         "unit": "GB/s",
         "frac": sb[dom] / dom_t / HBM_PEAK,
-        "traffic": None,
+        "traffic": None,  # filled below from the committed rocprofv3 --pmc measurement
         "algorithmic_bytes_per_launch": sb[dom],
         "avg_launch_us": stages_ms[dom] * 1e3,
         "layer_frac_of_roofline": max(B / HBM_PEAK, F / MFMA_BF16_PEAK) / t,
     }
+    try:
+        tj = json.load(open(args.traffic_json))
+        if tj.get("tokens") == T and "moe_stream_kernel" in tj.get("kernel", "") and bm == 16:
+            roofline["traffic"] = tj["traffic_bytes"]
+            roofline["traffic_source"] = os.path.relpath(args.traffic_json,
+                                                         os.path.dirname(args.traffic_json) +
+                                                         "/..")
+    except (OSError, ValueError, KeyError):
+        pass
     res = {
         "metric": "fused-MoE layer HBM GB/s, Qwen3-30B-A3B decode T=64 (bf16)",
         "value": B / t / 1e9,
