@@ -23,6 +23,7 @@ constexpr int kRouterWaves = 16;  // wavefronts per router workgroup
 
 // Softmax numerators, top-k and weights for one token whose logits lane j holds at
 // v[q] = logit[j + 64 q]. Writes topk_w/topk_ids[0..k). All lanes of the wavefront must call it.
+// Top-k by repeated argmax over the wavefront (largest p, lowest expert index among equal p).
 __device__ __forceinline__ void wave_select(float (&v)[kMaxM], int E, int top_k, int renorm,
                                             const int64_t* __restrict__ expert_map,
                                             float* __restrict__ out_w,
@@ -88,7 +89,8 @@ __global__ __launch_bounds__(256) void route_logits_kernel(
     const TLog* __restrict__ logits, int64_t T, int E, int64_t ld, int top_k, int renorm,
     const int64_t* __restrict__ expert_map, float* __restrict__ topk_w,
     int32_t* __restrict__ topk_ids) {
-    const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int w = threadIdx.x >> 6;
+    const int64_t t = (int64_t)blockIdx.x * 4 + w;
     if (t >= T) return;
     const int lane = threadIdx.x & 63;
     float v[kMaxM];
@@ -131,46 +133,78 @@ struct Chunk8<float> {
     }
 };
 
-// Gate GEMM + routing. Workgroup = kRouterWaves wavefronts and TB tokens; each wavefront computes
-// the logits of experts e = wave, wave + kRouterWaves, ... for the TB tokens (x slice held in
-// registers as fp32, the gate row streamed from L2 with one 16-byte load per lane per 512
-// columns), then wavefronts 0..TB-1 run the selection on the LDS logits of one token each.
-template <typename TIn, int NC, int TB>
+// Combines per-lane partials of N (power of two) different sums in one pass: at distance
+// s = 32, 16, ... a lane keeps half of its sums and adds its partner's values for them, until one
+// sum is left, then finishes with the plain butterfly. Partners are paired in exactly the order
+// of wave_sum_butterfly, so each result is bit-identical to butterflying that sum alone. Lane l
+// ends with the full sum number (l >> (6 - log2 N)).
+template <int N>
+__device__ __forceinline__ float wave_reduce_scatter(float (&acc)[N]) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int step = 0; step < 6; ++step) {
+        const int s = 32 >> step;
+        const int n = (N >> step) > 0 ? (N >> step) : 1;  // sums held before this step
+        if (n > 1) {
+            // lane-dependent choice made with bit masks on the values (a select between two
+            // array elements would become a dynamically indexed array in scratch memory)
+            const uint32_t up = (lane & s) ? 0xffffffffu : 0u;
+#pragma unroll
+            for (int k = 0; k < N / 2; ++k) {
+                if (k < n / 2) {
+                    const uint32_t lo = __float_as_uint(acc[k]);
+                    const uint32_t hi = __float_as_uint(acc[k + n / 2]);
+                    const float send = __uint_as_float((lo & up) | (hi & ~up));
+                    const float keep = __uint_as_float((hi & up) | (lo & ~up));
+                    acc[k] = keep + __shfl_xor(send, s);
+                }
+            }
+        } else {
+            acc[0] += __shfl_xor(acc[0], s);
+        }
+    }
+    return acc[0];
+}
+
+// Gate GEMM + routing for decode-sized batches: one workgroup of kRouterWaves wavefronts per
+// token. Wavefront w computes the per-lane partials of experts e = w + kRouterWaves*j (j < EPW),
+// holding x as fp32 in registers and streaming each gate row from L2 (one 16-byte load per lane
+// per 512 columns, GE experts in flight), combines its EPW sums with one reduce-scatter, and
+// wavefront 0 then selects from the logits in LDS.
+template <typename TIn, int NC, int EPW>
 __global__ __launch_bounds__(kRouterWaves * 64) void router_kernel(
     const TIn* __restrict__ x, const TIn* __restrict__ gw, int64_t T, int H, int E, int top_k,
     int renorm, const int64_t* __restrict__ expert_map, const float* __restrict__ bias,
     int logits_bf16, float* __restrict__ logits_out, float* __restrict__ topk_w,
     int32_t* __restrict__ topk_ids) {
 #pragma clang fp contract(off)
-    extern __shared__ float s_logits[];  // [TB][E]
+    __shared__ float s_logits[64 * kMaxM];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int64_t t0 = (int64_t)blockIdx.x * TB;
+    const int64_t t = blockIdx.x;
 
-    float xr[TB][NC * 8];
+    float xr[NC * 8];
 #pragma unroll
-    for (int tb = 0; tb < TB; ++tb) {
+    for (int c = 0; c < NC; ++c) {
+        const int h0 = c * 512 + lane * 8;
+        Chunk8<TIn> ch;
+        ch.zero();
+        if (h0 < H) ch.load(x + t * H + h0);
 #pragma unroll
-        for (int c = 0; c < NC; ++c) {
-            const int h0 = c * 512 + lane * 8;
-            Chunk8<TIn> ch;
-            ch.zero();
-            if (h0 < H && t0 + tb < T) ch.load(x + (t0 + tb) * H + h0);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) xr[tb][c * 8 + i] = ch.get(i);
-        }
+        for (int i = 0; i < 8; ++i) xr[c * 8 + i] = ch.get(i);
     }
 
-    // Experts e0 + j*kRouterWaves (j < GE) are in flight together: all their loads are issued
-    // before the first multiply.
     constexpr int kWords = sizeof(TIn) * 2;  // VGPRs per raw 8-element chunk
-    constexpr int kGe = ((TB == 1 ? 96 : 80) - TB * NC * 8) / (NC * kWords);
-    constexpr int GE = kGe < 1 ? 1 : (kGe > 4 ? 4 : kGe);
-    for (int e0 = wave; e0 < E; e0 += kRouterWaves * GE) {
+    constexpr int kGe = (96 - NC * 8) / (NC * kWords);
+    constexpr int GE0 = kGe < 1 ? 1 : (kGe > 4 ? 4 : kGe);
+    constexpr int GE = GE0 > EPW ? EPW : GE0;
+    float acc[EPW];
+#pragma unroll
+    for (int j0 = 0; j0 < EPW; j0 += GE) {
         Chunk8<TIn> gc[GE][NC];
 #pragma unroll
         for (int j = 0; j < GE; ++j) {
-            const int e = e0 + j * kRouterWaves;
+            const int e = wave + kRouterWaves * (j0 + j);
 #pragma unroll
             for (int c = 0; c < NC; ++c) {
                 const int h0 = c * 512 + lane * 8;
@@ -180,39 +214,35 @@ __global__ __launch_bounds__(kRouterWaves * 64) void router_kernel(
         }
 #pragma unroll
         for (int j = 0; j < GE; ++j) {
-            const int e = e0 + j * kRouterWaves;
-            if (e >= E) break;
+            float a = 0.0f;
 #pragma unroll
-            for (int tb = 0; tb < TB; ++tb) {
-                float acc = 0.0f;
+            for (int c = 0; c < NC; ++c) {
+                if (c * 512 + lane * 8 < H) {
 #pragma unroll
-                for (int c = 0; c < NC; ++c) {
-                    if (c * 512 + lane * 8 < H) {
-#pragma unroll
-                        for (int i = 0; i < 8; ++i)
-                            acc = __builtin_fmaf(xr[tb][c * 8 + i], gc[j][c].get(i), acc);
-                    }
-                }
-                float l = wave_sum_butterfly(acc);
-                if (bias) l = l + bias[e];
-                if (logits_bf16) l = round_bf16(l);
-                if (lane == 0) {
-                    s_logits[tb * E + e] = l;
-                    if (logits_out && t0 + tb < T) logits_out[(t0 + tb) * E + e] = l;
+                    for (int i = 0; i < 8; ++i) a = __builtin_fmaf(xr[c * 8 + i], gc[j][c].get(i), a);
                 }
             }
+            acc[j0 + j] = a;
         }
+    }
+    float l = wave_reduce_scatter<EPW>(acc);
+    constexpr int kShift = (EPW >= 64) ? 0 : (EPW == 32 ? 1 : EPW == 16 ? 2 : EPW == 8 ? 3
+                                                          : EPW == 4 ? 4 : EPW == 2 ? 5 : 6);
+    const int e = wave + kRouterWaves * (lane >> kShift);
+    if ((lane & ((1 << kShift) - 1)) == 0 && e < E) {
+        if (bias) l = l + bias[e];
+        if (logits_bf16) l = round_bf16(l);
+        s_logits[e] = l;
+        if (logits_out) logits_out[t * E + e] = l;
     }
     __syncthreads();
 
-    for (int tb = wave; tb < TB; tb += kRouterWaves) {
-        const int64_t t = t0 + tb;
-        if (t >= T) break;
+    if (wave == 0) {
         float v[kMaxM];
 #pragma unroll
         for (int q = 0; q < kMaxM; ++q) {
-            int e = lane + 64 * q;
-            v[q] = e < E ? s_logits[tb * E + e] : 0.0f;
+            int ee = lane + 64 * q;
+            v[q] = ee < E ? s_logits[ee] : 0.0f;
         }
         wave_select(v, E, top_k, renorm, expert_map, topk_w + t * top_k, topk_ids + t * top_k);
     }
@@ -286,24 +316,13 @@ __global__ __launch_bounds__(kTileWaves * 64) void router_tile_kernel(
                 }
             }
         }
-        // transposed reduce-scatter: after the step at distance s, lane l holds the pairs whose
-        // index bits above log2(s) match its own; the last lane holding pair p is l == p.
-#pragma unroll
-        for (int s = 32, n = 64; s >= 1; s >>= 1, n >>= 1) {
-            const bool upper = (lane & s) != 0;
-#pragma unroll
-            for (int k = 0; k < n / 2; ++k) {
-                const float send = upper ? acc[k] : acc[k + n / 2];
-                const float keep = upper ? acc[k + n / 2] : acc[k];
-                acc[k] = keep + __shfl_xor(send, s);
-            }
-        }
+        // transposed reduce-scatter: lane l ends with the sum of pair p == l
+        float l = wave_reduce_scatter<kTT * kEG>(acc);
         const int tt = lane / kEG, e = grp * kEG + lane % kEG;
         if (e < E) {
-            float l = acc[0];
             if (bias) l = l + bias[e];
             if (logits_bf16) l = round_bf16(l);
-            s_logits[tt * E + e] = l;
+            s_logits[tt * 512 + e] = l;
             if (logits_out && t0 + tt < T) logits_out[(t0 + tt) * E + e] = l;
         }
     }
@@ -316,7 +335,7 @@ __global__ __launch_bounds__(kTileWaves * 64) void router_tile_kernel(
 #pragma unroll
         for (int q = 0; q < kMaxM; ++q) {
             int e = lane + 64 * q;
-            v[q] = e < E ? s_logits[tb * E + e] : 0.0f;
+            v[q] = e < E ? s_logits[tb * 512 + e] : 0.0f;
         }
         wave_select(v, E, top_k, renorm, expert_map, topk_w + t * top_k, topk_ids + t * top_k);
     }
@@ -334,31 +353,40 @@ hipError_t launch_router_tile(const void* x, const void* gw, int64_t T, int H, i
     return hipGetLastError();
 }
 
-template <typename TIn, int NC, int TB>
-hipError_t launch_router_tb(const void* x, const void* gw, int64_t T, int H, int E, int top_k,
-                            int renorm, const int64_t* expert_map, const float* bias,
-                            int logits_bf16, float* logits_out, float* w, int32_t* ids,
-                            hipStream_t stream) {
-    const int64_t blocks = (T + TB - 1) / TB;
-    const size_t lds = sizeof(float) * TB * E;
-    hipLaunchKernelGGL((router_kernel<TIn, NC, TB>), dim3((unsigned)blocks),
-                       dim3(kRouterWaves * 64), lds, stream, (const TIn*)x, (const TIn*)gw, T, H,
-                       E, top_k, renorm, expert_map, bias, logits_bf16, logits_out, w, ids);
+template <typename TIn, int NC, int EPW>
+hipError_t launch_router_decode(const void* x, const void* gw, int64_t T, int H, int E, int top_k,
+                                int renorm, const int64_t* expert_map, const float* bias,
+                                int logits_bf16, float* logits_out, float* w, int32_t* ids,
+                                hipStream_t stream) {
+    hipLaunchKernelGGL((router_kernel<TIn, NC, EPW>), dim3((unsigned)T), dim3(kRouterWaves * 64),
+                       0, stream, (const TIn*)x, (const TIn*)gw, T, H, E, top_k, renorm,
+                       expert_map, bias, logits_bf16, logits_out, w, ids);
     return hipGetLastError();
 }
 
-// Decode-sized batches: one token per workgroup, x in registers (more workgroups, lower latency).
-// Larger batches: 8-token tiles with the transposed reduction.
+// Decode-sized batches: one token per workgroup (more workgroups, lower latency), experts per
+// wavefront rounded up to a power of two. Larger batches: 8-token tiles.
 template <typename TIn, int NC>
 hipError_t launch_router_nc(const void* x, const void* gw, int64_t T, int H, int E, int top_k,
                             int renorm, const int64_t* expert_map, const float* bias,
                             int logits_bf16, float* logits_out, float* w, int32_t* ids,
                             hipStream_t stream) {
-    if (T <= 256)
-        return launch_router_tb<TIn, NC, 1>(x, gw, T, H, E, top_k, renorm, expert_map, bias,
-                                            logits_bf16, logits_out, w, ids, stream);
-    return launch_router_tile<TIn, NC>(x, gw, T, H, E, top_k, renorm, expert_map, bias,
-                                       logits_bf16, logits_out, w, ids, stream);
+    if (T > 256)
+        return launch_router_tile<TIn, NC>(x, gw, T, H, E, top_k, renorm, expert_map, bias,
+                                           logits_bf16, logits_out, w, ids, stream);
+    const int epw = (E + kRouterWaves - 1) / kRouterWaves;
+#define TSM_DEC(N)                                                                             \
+    if (epw <= N)                                                                              \
+        return launch_router_decode<TIn, NC, N>(x, gw, T, H, E, top_k, renorm, expert_map,     \
+                                                bias, logits_bf16, logits_out, w, ids, stream);
+    TSM_DEC(1)
+    TSM_DEC(2)
+    TSM_DEC(4)
+    TSM_DEC(8)
+    TSM_DEC(16)
+    TSM_DEC(32)
+#undef TSM_DEC
+    return hipErrorInvalidValue;
 }
 
 template <typename TIn>
