@@ -162,16 +162,16 @@ def main():
         height."""
         xs = inputs(T, 1000 + T)
         numel = T * K_TOP
-        bm = int(lib.tsm_moe_block_m(T, H, I, E, K_TOP, 1))
-        mp = int(lib.tsm_moe_max_padded(numel, E, bm))
-        nws = int(lib.tsm_moe_align_workspace_size(numel, E, bm))
+        bm = int(lib.tsm_moe_block_m(T, H, I, E, K_TOP, 1))  # 0: expert-major, no permutation
+        mp = int(lib.tsm_moe_max_padded(numel, E, bm)) if bm else numel
+        nws = int(lib.tsm_moe_align_workspace_size(numel, E, bm)) if bm else 0
         st = []
         for i in range(L):
             st.append(dict(
                 w=torch.empty(T, K_TOP, dtype=torch.float32, device=dev),
                 ids=torch.empty(T, K_TOP, dtype=torch.int32, device=dev),
                 sorted_ids=torch.empty(mp, dtype=torch.int32, device=dev),
-                eids=torch.empty(mp // bm, dtype=torch.int32, device=dev),
+                eids=torch.empty(mp // bm if bm else 1, dtype=torch.int32, device=dev),
                 total=torch.empty(1, dtype=torch.int32, device=dev),
                 aws=torch.empty(max(nws, 1), dtype=torch.uint8, device=dev),
                 act=torch.empty(mp, I, dtype=torch.bfloat16, device=dev),
@@ -193,12 +193,22 @@ def main():
 
         def gate_up(i):
             c = st[i]
+            if bm == 0:
+                check(lib.tsm_moe_expert_gate_up(ptr(xs[i]), ptr(packed[i][0]), ptr(c["ids"]),
+                                                 numel, K_TOP, H, I, E, 1, ptr(c["act"]),
+                                                 cur()), "gate_up")
+                return
             check(lib.tsm_moe_gemm_gate_up(ptr(xs[i]), ptr(packed[i][0]), ptr(c["sorted_ids"]),
                                            ptr(c["eids"]), ptr(c["total"]), numel, K_TOP, H, I,
                                            E, bm, 1, ptr(c["act"]), cur()), "gate_up")
 
         def down(i):
             c = st[i]
+            if bm == 0:
+                check(lib.tsm_moe_expert_down(ptr(c["act"]), ptr(packed[i][1]), ptr(c["w"]),
+                                              ptr(c["ids"]), numel, H, I, E, 1, ptr(c["rows"]),
+                                              cur()), "down")
+                return
             check(lib.tsm_moe_gemm_down(ptr(c["act"]), ptr(packed[i][1]), ptr(c["w"]),
                                         ptr(c["sorted_ids"]), ptr(c["eids"]), ptr(c["total"]),
                                         numel, H, I, E, bm, 1, ptr(c["rows"]), cur()), "down")
@@ -210,6 +220,8 @@ def main():
 
         stages = [("router", router), ("align", align), ("gate_up", gate_up), ("down", down),
                   ("combine", combine)]
+        if bm == 0:
+            stages = [st_ for st_ in stages if st_[0] != "align"]
         for i in range(L):
             for _, fn in stages:
                 fn(i)
@@ -247,11 +259,14 @@ def main():
     t = ms * 1e-3
     sb = stage_bytes(T, n_touched)
     sf = stage_flops(T)
+    if "align" not in stages_ms:
+        sb.pop("align")
     dom = "gate_up"
     dom_t = stages_ms[dom] * 1e-3
     roofline = {
-        "kernel": "moe_stream_kernel<gate_up, packed> (gate_up GEMM + SwiGLU epilogue)"
-                  if bm == 16 else "moe_tile_kernel<gate_up> (gate_up GEMM + SwiGLU epilogue)",
+        "kernel": {0: "moe_expert_kernel<gate_up, packed> (gate_up GEMM + SwiGLU epilogue)",
+                   16: "moe_stream_kernel<gate_up, packed> (gate_up GEMM + SwiGLU epilogue)"}.get(
+                       bm, "moe_tile_kernel<gate_up> (gate_up GEMM + SwiGLU epilogue)"),
         "bound": "hbm",
         "achieved": sb[dom] / dom_t / 1e9,
         "peak": HBM_PEAK / 1e9,
@@ -264,7 +279,8 @@ def main():
     }
     try:
         tj = json.load(open(args.traffic_json))
-        if tj.get("tokens") == T and "moe_stream_kernel" in tj.get("kernel", "") and bm == 16:
+        kname = {0: "moe_expert_kernel", 16: "moe_stream_kernel"}.get(bm, "moe_tile_kernel")
+        if tj.get("tokens") == T and kname in tj.get("kernel", ""):
             roofline["traffic"] = tj["traffic_bytes"]
             roofline["traffic_source"] = os.path.relpath(args.traffic_json,
                                                          os.path.dirname(args.traffic_json) +

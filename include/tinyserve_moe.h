@@ -104,7 +104,8 @@ int tsm_silu_and_mul(const void* gate, int64_t gate_stride, const void* up, int6
 /*
  * Tile height (rows per expert tile) fused_moe uses for a batch of T tokens with the given weight
  * layout (TSM_LAYOUT_*). The reference picks 16 when T*k <= 4E, else 64 (tinykernels.py:1779);
- * this build picks from its own kernel table (16 / 64, and 128 for packed weights).
+ * this build picks from its own kernel table: 0 = the expert-major stages below (no tiles, no
+ * permutation), else 16 / 64, and 128 for packed weights.
  */
 int tsm_moe_block_m(int64_t T, int H, int I, int E, int top_k, int weight_layout);
 
@@ -145,6 +146,21 @@ int tsm_moe_gemm_down(const void* act, const void* w2, const float* topk_w,
                       int64_t numel, int H, int I, int E, int block_m, int weight_layout,
                       void* rows, hipStream_t stream);
 int tsm_moe_combine(const void* rows, int64_t T, int H, int top_k, void* out, hipStream_t stream);
+
+/*
+ * Expert-major stages used by fused_moe for decode-sized batches (tsm_moe_block_m() == 0): no
+ * permutation step; each workgroup finds its expert's assignments by scanning topk_ids [numel]
+ * (stable flat order, as moe_align_block_size orders them), and act [numel, I] holds the
+ * activations in expert-sorted order (expert e's rows start at the number of assignments to
+ * experts < e). gate_up writes act; down writes rows [numel, H] (zeros for ids outside [0, E)).
+ * Requires numel <= 4096, H and I multiples of 128 with H/128, I/128 <= 16.
+ */
+int tsm_moe_expert_gate_up(const void* x, const void* w13, const int32_t* topk_ids,
+                           int64_t numel, int top_k, int H, int I, int E, int weight_layout,
+                           void* act, hipStream_t stream);
+int tsm_moe_expert_down(const void* act, const void* w2, const float* topk_w,
+                        const int32_t* topk_ids, int64_t numel, int H, int I, int E,
+                        int weight_layout, void* rows, hipStream_t stream);
 
 /*
  * Whole SparseMoE.forward on one GPU (serve.py:1076-1087 at TP=1): fused router then fused_moe.

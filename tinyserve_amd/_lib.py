@@ -39,6 +39,8 @@ def _load():
         "tsm_fused_moe": ([P, P, P, P, P, I64, I32, I32, I32, I32, I32, P, P, SZ, P], I32),
         "tsm_moe_gemm_gate_up": ([P, P, P, P, P, I64, I32, I32, I32, I32, I32, I32, P, P], I32),
         "tsm_moe_gemm_down": ([P, P, P, P, P, P, I64, I32, I32, I32, I32, I32, P, P], I32),
+        "tsm_moe_expert_gate_up": ([P, P, P, I64, I32, I32, I32, I32, I32, P, P], I32),
+        "tsm_moe_expert_down": ([P, P, P, P, I64, I32, I32, I32, I32, P, P], I32),
         "tsm_moe_pack_weights": ([P, I64, I32, I32, I32, P, P], I32),
         "tsm_fused_moe_packed": ([P, P, P, P, P, I64, I32, I32, I32, I32, I32, P, P, SZ, P], I32),
         "tsm_moe_forward_packed": ([P, P, P, P, P, P, I64, I32, I32, I32, I32, I32, I32, I32, P, P,

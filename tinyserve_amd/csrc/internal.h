@@ -50,5 +50,25 @@ inline int64_t active_tile_bound(int64_t numel, int E, int block_m) {
 bool launch_tile_gate_up(GemmArgs g, int block_m, hipStream_t stream);
 bool launch_tile_down(GemmArgs g, int block_m, hipStream_t stream);
 
+// Expert-major decode kernels (no permutation step): assignments per expert are found by scanning
+// the ids. act is compact: rows [0, numel) in expert-sorted order.
+constexpr int kExpertMaxRows = 4096;  // numel limit of this path (LDS row list)
+struct ExpertArgs {
+    const uint16_t* A;      // gate_up: x [T, K]; down: act [numel, K]
+    const uint16_t* B;      // gate_up: w13; down: w2 (reference or packed layout)
+    uint16_t* C;            // gate_up: act [numel, N]; down: rows [numel, N]
+    const float* topk_w;    // down: [numel]
+    const int32_t* ids;     // [numel]
+    int64_t numel;
+    int top_k;
+    int N;
+    int K;
+    int E;
+    int n_tiles;
+};
+bool expert_path_supported(int64_t numel, int H, int I, int E);
+bool launch_expert_gate_up(ExpertArgs g, bool packed, hipStream_t stream);
+bool launch_expert_down(ExpertArgs g, bool packed, hipStream_t stream);
+
 inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 }  // namespace tsm

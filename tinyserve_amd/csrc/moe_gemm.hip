@@ -249,15 +249,19 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const bf16_t* __restrict_
 }
 
 // ---- kernel table --------------------------------------------------------------------------
-// Tile height per batch size. Reference-layout weights: 16-row weight-streaming tiles while
-// numel <= 4E (the reference's own BLOCK_M switch, tinykernels.py:1779), else 64-row LDS tiles.
-// Packed weights: 16-row tiles up to 4E, 64-row pipelined tiles up to 32E, 128-row above.
+// Tile height per batch size. block_m == 0: expert-major weight streaming (moe_expert.hip, no
+// permutation step) for 2E <= numel <= 16E; below 2E most experts are empty and the 16-row
+// streaming tiles over the permuted rows launch fewer workgroups. Otherwise reference-layout weights use 64-row LDS tiles
+// (the reference's BLOCK_M switch is at 4E, tinykernels.py:1779); packed weights use 64-row
+// pipelined tiles up to 32E and 128-row above.
 struct Plan {
     int block_m;
 };
 
-Plan plan_for(int64_t T, int E, int top_k, bool packed) {
+Plan plan_for(int64_t T, int H, int I, int E, int top_k, bool packed) {
     const int64_t numel = T * top_k;
+    if (numel >= 2ll * E && numel <= 16ll * E && expert_path_supported(numel, H, I, E))
+        return Plan{0};
     if (numel <= 4ll * E) return Plan{16};
     if (!packed || numel <= 32ll * E) return Plan{64};
     return Plan{128};
@@ -275,7 +279,11 @@ Layout layout_for(int64_t T, int H, int I, int E, int top_k, bool with_route) {
     const int64_t numel = T * top_k;
     int64_t mp = 0, tiles = 0;
     for (bool packed : {false, true}) {
-        const int bm = plan_for(T, E, top_k, packed).block_m;
+        const int bm = plan_for(T, H, I, E, top_k, packed).block_m;
+        if (bm == 0) {  // expert-major path: compact activations, no permutation buffers
+            mp = std::max(mp, numel);
+            continue;
+        }
         const int64_t m = max_padded_rows(numel, E, bm);
         mp = std::max(mp, m);
         tiles = std::max(tiles, m / bm);
@@ -332,6 +340,7 @@ GemmArgs gemm_args(const bf16_t* A, const bf16_t* B, bf16_t* C, const float* top
 }
 
 bool block_m_supported(int block_m, bool packed) {
+    if (block_m == 0) return false;  // the expert-major path has its own entry points
     return block_m == 16 || block_m == 64 || (packed && block_m == 128);
 }
 
@@ -381,12 +390,51 @@ void launch_combine(const bf16_t* rows, int64_t T, int H, int top_k, bf16_t* out
                        stream, rows, out, T, H, top_k);
 }
 
+ExpertArgs expert_args(const bf16_t* A, const bf16_t* B, bf16_t* C, const float* topk_w,
+                       const int32_t* ids, int64_t numel, int top_k, int N, int K, int E) {
+    ExpertArgs g{};
+    g.A = A;
+    g.B = B;
+    g.C = C;
+    g.topk_w = topk_w;
+    g.ids = ids;
+    g.numel = numel;
+    g.top_k = top_k;
+    g.N = N;
+    g.K = K;
+    g.E = E;
+    return g;
+}
+
+bool launch_expert_stages(const bf16_t* x, const bf16_t* w13, const bf16_t* w2,
+                          const float* topk_w, const int32_t* ids, int64_t numel, int top_k,
+                          int H, int I, int E, bool packed, bf16_t* act, bf16_t* rows,
+                          hipStream_t stream) {
+    if (!launch_expert_gate_up(expert_args(x, w13, act, nullptr, ids, numel, top_k, I, H, E),
+                               packed, stream))
+        return false;
+    return launch_expert_down(expert_args(act, w2, rows, topk_w, ids, numel, 1, H, I, E), packed,
+                              stream);
+}
+
 // Everything after routing: align, gate_up + SwiGLU, down * weight, k-sum.
 int run_experts(const void* x, const void* w13, const void* w2, const float* topk_w,
                 const int32_t* topk_ids, int64_t T, int H, int I, int E, int top_k, int sum_topk,
                 bool packed, void* out, char* ws, const Layout& L, hipStream_t stream) {
-    const Plan pl = plan_for(T, E, top_k, packed);
+    const Plan pl = plan_for(T, H, I, E, top_k, packed);
     const int64_t numel = T * top_k;
+    bf16_t* rows = sum_topk ? reinterpret_cast<bf16_t*>(ws + L.rows) : (bf16_t*)out;
+    if (pl.block_m == 0) {
+        TSM_REQUIRE(L.rows - L.act >= sizeof(bf16_t) * (size_t)(numel * I), TSM_E_WORKSPACE,
+                    "internal: workspace layout does not fit the expert-major path");
+        bf16_t* act = reinterpret_cast<bf16_t*>(ws + L.act);
+        TSM_REQUIRE(launch_expert_stages((const bf16_t*)x, (const bf16_t*)w13,
+                                         (const bf16_t*)w2, topk_w, topk_ids, numel, top_k, H,
+                                         I, E, packed, act, rows, stream),
+                    TSM_E_SHAPE, "internal: no expert-major kernel for H=%d I=%d", H, I);
+        if (sum_topk) launch_combine(rows, T, H, top_k, (bf16_t*)out, stream);
+        return check_launch("fused_moe kernels");
+    }
     {   // the workspace regions must hold this plan's buffers (host-side guard, no launch if not)
         const int64_t mp = max_padded_rows(numel, E, pl.block_m);
         const bool fits = L.expert_ids - L.sorted >= sizeof(int32_t) * (size_t)mp &&
@@ -399,7 +447,6 @@ int run_experts(const void* x, const void* w13, const void* w2, const float* top
     int32_t* eids = reinterpret_cast<int32_t*>(ws + L.expert_ids);
     int32_t* total = reinterpret_cast<int32_t*>(ws + L.total);
     bf16_t* act = reinterpret_cast<bf16_t*>(ws + L.act);
-    bf16_t* rows = sum_topk ? reinterpret_cast<bf16_t*>(ws + L.rows) : (bf16_t*)out;
 
     (void)launch_align(topk_ids, numel, E, pl.block_m, sorted, eids, total, ws + L.hist, stream);
     launch_gate_up((const bf16_t*)x, (const bf16_t*)w13, sorted, eids, total, numel, top_k, H, I,
@@ -418,7 +465,7 @@ using namespace tsm;
 extern "C" int tsm_moe_block_m(int64_t T, int H, int I, int E, int top_k, int weight_layout) {
     (void)H;
     (void)I;
-    return plan_for(T, E, top_k, weight_layout != 0).block_m;
+    return plan_for(T, H, I, E, top_k, weight_layout != 0).block_m;
 }
 
 extern "C" int tsm_silu_and_mul(const void* gate, int64_t gate_stride, const void* up,
@@ -571,4 +618,42 @@ extern "C" int tsm_moe_combine(const void* rows, int64_t T, int H, int top_k, vo
     TSM_REQUIRE(rows && out, TSM_E_ARG, "null pointer argument");
     launch_combine((const bf16_t*)rows, T, H, top_k, (bf16_t*)out, stream);
     return check_launch("combine");
+}
+
+extern "C" int tsm_moe_expert_gate_up(const void* x, const void* w13, const int32_t* topk_ids,
+                                      int64_t numel, int top_k, int H, int I, int E,
+                                      int weight_layout, void* act, hipStream_t stream) {
+    clear_error();
+    int rc = check_moe_shapes(numel / (top_k > 0 ? top_k : 1), H, I, E, top_k);
+    if (rc) return rc;
+    TSM_REQUIRE(expert_path_supported(numel, H, I, E), TSM_E_SHAPE,
+                "expert-major path unsupported for numel=%lld H=%d I=%d E=%d", (long long)numel,
+                H, I, E);
+    if (numel == 0) return TSM_OK;
+    TSM_REQUIRE(x && w13 && topk_ids && act, TSM_E_ARG, "null pointer argument");
+    TSM_REQUIRE(launch_expert_gate_up(expert_args((const bf16_t*)x, (const bf16_t*)w13,
+                                                  (bf16_t*)act, nullptr, topk_ids, numel, top_k,
+                                                  I, H, E),
+                                      weight_layout != 0, stream),
+                TSM_E_SHAPE, "no expert-major gate_up kernel for H=%d", H);
+    return check_launch("expert gate_up");
+}
+
+extern "C" int tsm_moe_expert_down(const void* act, const void* w2, const float* topk_w,
+                                   const int32_t* topk_ids, int64_t numel, int H, int I, int E,
+                                   int weight_layout, void* rows, hipStream_t stream) {
+    clear_error();
+    int rc = check_moe_shapes(numel, H, I, E, 1);
+    if (rc) return rc;
+    TSM_REQUIRE(expert_path_supported(numel, H, I, E), TSM_E_SHAPE,
+                "expert-major path unsupported for numel=%lld H=%d I=%d E=%d", (long long)numel,
+                H, I, E);
+    if (numel == 0) return TSM_OK;
+    TSM_REQUIRE(act && w2 && topk_w && topk_ids && rows, TSM_E_ARG, "null pointer argument");
+    TSM_REQUIRE(launch_expert_down(expert_args((const bf16_t*)act, (const bf16_t*)w2,
+                                               (bf16_t*)rows, topk_w, topk_ids, numel, 1, H, I,
+                                               E),
+                                   weight_layout != 0, stream),
+                TSM_E_SHAPE, "no expert-major down kernel for I=%d", I);
+    return check_launch("expert down");
 }
