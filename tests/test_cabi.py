@@ -46,7 +46,10 @@ def test_sizes(lib):
     assert lib.tsm_moe_max_padded(4, 3, 4) == 16              # docstring example
     lib.tsm_fused_moe_workspace_size.restype = ctypes.c_size_t
     lib.tsm_fused_moe_workspace_size.argtypes = [ctypes.c_int64] + [ctypes.c_int] * 4
-    assert lib.tsm_fused_moe_workspace_size(64, 2048, 768, 128, 8) > 2448 * 768 * 2
+    # T=64 runs expert-major (compact activations, one row per assignment) plus the per-slot rows
+    assert lib.tsm_fused_moe_workspace_size(64, 2048, 768, 128, 8) >= 512 * (768 + 2048) * 2
+    # T=8192 runs the tiled path: activations for every padded row
+    assert lib.tsm_fused_moe_workspace_size(8192, 2048, 768, 128, 8) >= 73664 * 768 * 2
     lib.tsm_abi_version.restype = ctypes.c_int
     assert lib.tsm_abi_version() == 1
 
