@@ -235,7 +235,7 @@ def test_pack_layout_matches_definition(dev, tsm):
     assert torch.equal(p2.cpu(), ref(w2.cpu(), False))
 
 
-@pytest.mark.parametrize("T", [1, 8, 64, 256, 2048])
+@pytest.mark.parametrize("T", [1, 8, 64, 256, 512, 2048, 4096])
 def test_packed_path_bitexact_with_reference_layout(dev, tsm, qwen_layer, T):
     """The packed kernels consume the same k order per lane as the reference-layout kernels, so
     outputs are identical bit for bit; and both match the oracle."""
@@ -258,11 +258,13 @@ def test_packed_expert_parallel_and_tiny(dev, tsm, qwen_layer):
     p13, p2 = tsm.pack_moe_weights(w13, w2)
     emap = torch.arange(128, dtype=torch.int64, device=dev)
     emap[::2] = -1
-    x = xrand(50, 2048, dev, 77)
-    w, ids, _ = tsm.moe_router(x, gw, 8, True, emap)
-    out = tsm.fused_moe_packed(x, p13, p2, w, ids)
-    ref = moe_reference(x.cpu(), w13c, w2c, w.cpu(), ids.cpu().long())
-    assert_close(out, ref, "packed EP")
+    for T in (50, 700):  # weight-streaming and 128-row tile kernels
+        x = xrand(T, 2048, dev, 77)
+        w, ids, _ = tsm.moe_router(x, gw, 8, True, emap)
+        out = tsm.fused_moe_packed(x, p13, p2, w, ids)
+        assert torch.equal(out, tsm.fused_moe(x, w13, w2, w, ids)), f"packed EP T={T}"
+        ref = moe_reference(x.cpu(), w13c, w2c, w.cpu(), ids.cpu().long())
+        assert_close(out, ref, f"packed EP T={T}")
     from oracle.moe_oracle import make_layer
     x, gw, w13, w2 = make_layer(37, 256, 8, 512, torch.bfloat16, seed=0, device=dev)
     p13, p2 = tsm.pack_moe_weights(w13, w2)
@@ -270,3 +272,10 @@ def test_packed_expert_parallel_and_tiny(dev, tsm, qwen_layer):
     out = tsm.fused_moe_packed(x, p13, p2, w, ids)
     ref = moe_reference(x.cpu(), w13.cpu(), w2.cpu(), w.cpu(), ids.cpu().long())
     assert_close(out, ref, "packed tiny")
+    # tiny shape at a tile-kernel batch (K = 256 and 512: short pipelines)
+    x = xrand(2048, 256, dev, 78)
+    w, ids, _ = tsm.moe_router(x, gw, 2, True)
+    out = tsm.fused_moe_packed(x, p13, p2, w, ids)
+    assert torch.equal(out, tsm.fused_moe(x, w13, w2, w, ids))
+    ref = moe_reference(x.cpu(), w13.cpu(), w2.cpu(), w.cpu(), ids.cpu().long())
+    assert_close(out, ref, "packed tiny T=2048")

@@ -19,13 +19,10 @@ __device__ __forceinline__ float bf16_to_f32(bf16_t v) {
     return __uint_as_float(((uint32_t)v) << 16);
 }
 
-// Round to nearest even; NaN stays a quiet NaN. Same rule as torch's float -> bfloat16 cast.
-__host__ __device__ __forceinline__ bf16_t f32_to_bf16(float f) {
-    uint32_t u;
-    memcpy(&u, &f, 4);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return (bf16_t)((u >> 16) | 0x40);
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return (bf16_t)(u >> 16);
+// Round to nearest even (the hardware conversion, v_cvt_pk_bf16_f32; same rule as torch's
+// float -> bfloat16 cast).
+__device__ __forceinline__ bf16_t f32_to_bf16(float f) {
+    return __builtin_bit_cast(bf16_t, (__bf16)f);
 }
 
 __device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
@@ -34,8 +31,23 @@ __device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to
 __device__ __forceinline__ float lo_bf16(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float hi_bf16(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
-    return (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, bf16x2));
+}
+
+// SwiGLU with the reference's rounding points (tinykernels.py:293-297; the reference stores gate
+// and up as bf16 and F.silu returns bf16): silu(g) = g * sigmoid(g) is rounded to bf16 before the
+// multiply by u. sigmoid uses the hardware exp2 and reciprocal (about 1 fp32 ulp each), so the
+// rounded silu equals that of an exactly rounded sigmoid except within a few fp32 ulps of a bf16
+// rounding boundary. Every kernel that applies SwiGLU calls this one definition, so all weight
+// layouts and tile shapes give identical bits.
+__device__ __forceinline__ float swiglu_bf16(float g, float u) {
+    g = round_bf16(g);
+    u = round_bf16(u);
+    const float s = round_bf16(g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)));
+    return s * u;
 }
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }

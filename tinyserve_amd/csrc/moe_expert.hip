@@ -22,13 +22,6 @@
 namespace tsm {
 namespace {
 
-__device__ __forceinline__ float swiglu_e(float g, float u) {
-    g = round_bf16(g);
-    u = round_bf16(u);
-    const float s = round_bf16(g / (1.0f + __expf(-g)));
-    return s * u;
-}
-
 constexpr int kMaxBucketsE = 513;
 
 template <int S, int NB, int WN, bool GATEUP, bool PACKED, bool SPEC>
@@ -168,7 +161,7 @@ __global__ __launch_bounds__(256 * WN, 2) void moe_expert_kernel(ExpertArgs p) {
             }
             if (GATEUP) {
                 p.C[(int64_t)(start + m0 + row) * p.N + n_tile * 16 + col] =
-                    f32_to_bf16(swiglu_e(v[0], v[1]));
+                    f32_to_bf16(swiglu_bf16(v[0], v[1]));
             } else {
                 const int flat = s_rows[m0 + row];
                 const float w = p.topk_w[flat];

@@ -23,14 +23,6 @@ constexpr int BK = 64;        // K elements per main-loop step
 constexpr int LDK = BK + 8;   // LDS row stride in bf16 elements (144 bytes: 16-byte aligned rows)
 
 
-// bf16(silu(g)) * u with g, u first rounded to bf16 (the reference stores gate/up as bf16).
-__device__ __forceinline__ float swiglu(float g, float u) {
-    g = round_bf16(g);
-    u = round_bf16(u);
-    const float s = round_bf16(g / (1.0f + __expf(-g)));
-    return s * u;
-}
-
 // Workgroup tile BM x BN of C (for gate_up, BN counts B rows: BN/2 gate rows + the matching BN/2
 // up rows, so BN/2 activation columns), 4 wavefronts in a WM x WN grid, 16x16x32 bf16 MFMA,
 // A and B staged through double-buffered LDS with a register prefetch of the next K step.
@@ -193,7 +185,7 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(GemmArgs p) {
                 for (int g = 0; g < FN / 2; ++g) {
                     const int col = n_tile * (BN / 2) + wn * OW + g * 16 + (lane & 15);
                     p.C[(int64_t)grow * p.N + col] =
-                        f32_to_bf16(swiglu(acc[f][g][i], acc[f][g + FN / 2][i]));
+                        f32_to_bf16(swiglu_bf16(acc[f][g][i], acc[f][g + FN / 2][i]));
                 }
             } else {
                 const int flat = p.sorted_ids[grow];
@@ -241,10 +233,8 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const bf16_t* __restrict_
     const int64_t row = blockIdx.y;
     for (int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x; c < N;
          c += (int64_t)gridDim.x * 256) {
-        const float g = bf16_to_f32(gate[row * gs + c]);
-        const float u = bf16_to_f32(up[row * us + c]);
-        const float s = round_bf16(g / (1.0f + __expf(-g)));
-        out[row * os + c] = f32_to_bf16(s * u);
+        out[row * os + c] = f32_to_bf16(
+            swiglu_bf16(bf16_to_f32(gate[row * gs + c]), bf16_to_f32(up[row * us + c])));
     }
 }
 

@@ -21,13 +21,6 @@
 namespace tsm {
 namespace {
 
-__device__ __forceinline__ float swiglu_ref(float g, float u) {
-    g = round_bf16(g);
-    u = round_bf16(u);
-    const float s = round_bf16(g / (1.0f + __expf(-g)));
-    return s * u;
-}
-
 // S: MFMA k-steps per wavefront (K = 4 * 32 * S). NB: 16-row B blocks per wavefront; for gate_up
 // NB = 2 (one gate block and the matching up block -> 16 activation columns). WN: groups of 4
 // wavefronts, each group taking the next NB blocks (down GEMM only).
@@ -126,7 +119,7 @@ __global__ __launch_bounds__(256 * WN, 2 / WN) void moe_stream_kernel(GemmArgs p
         v[nb] = ((red[0][bb][l][i] + red[1][bb][l][i]) + red[2][bb][l][i]) + red[3][bb][l][i];
     }
     if (GATEUP) {
-        p.C[(int64_t)(m0 + row) * p.N + n_tile * 16 + col] = f32_to_bf16(swiglu_ref(v[0], v[1]));
+        p.C[(int64_t)(m0 + row) * p.N + n_tile * 16 + col] = f32_to_bf16(swiglu_bf16(v[0], v[1]));
     } else {
         const int flat = p.sorted_ids[m0 + row];
         if (flat < p.numel) {

@@ -1,18 +1,24 @@
 // LDS-pipelined grouped GEMMs for prefill-sized batches (64/128-row expert tiles).
 //
 // Workgroup tile: BM expert-sorted rows x 256 rows of B (gate_up: 8 gate + 8 up 16-row blocks ->
-// 128 activation columns; down: 256 output columns), 4 wavefronts in a 2 x 2 grid, each owning a
-// (BM/2) x 128 block of C in 16x16x32 bf16 MFMA accumulators.
+// 128 activation columns; down: 256 output columns), 8 wavefronts in a (BM/64) x (512/BM) grid,
+// each owning a 64-row block of C in 16x16x32 bf16 MFMA accumulators.
 //
 // Operands reach LDS through direct global->LDS loads (global_load_lds_dwordx4: 64 lanes x 16 B,
-// written to LDS in lane order), so LDS holds every 16-row x 32-k operand block in exactly the
-// order an MFMA lane reads it (ds_read_b128 at lane*16, no bank conflicts, no register staging):
-//   - B comes from the MFMA-tiled (packed) weights, where such a block is 1 KiB of contiguous
-//     memory;
-//   - A rows are gathered per lane (gate_up: x[sorted_id / top_k]; down: activation rows), each
-//     lane fetching the 16 bytes it will later read back.
-// K is consumed in stages of 64 (two MFMA k-steps) through a 3-deep LDS ring: the loads of stage
-// s+2 are issued before stage s is computed.
+// written to LDS at lane*16), in stages of 64 k through a ring of NS stages:
+//   - B comes from the MFMA-tiled (packed) weights, where a 16-row x 32-k operand block is 1 KiB
+//     of contiguous memory already in MFMA lane order;
+//   - A rows (gate_up: gathered x[sorted_id / top_k]; down: activation rows) are loaded as whole
+//     128-byte lines, 8 rows per instruction: through the texture path a gather of whole lines
+//     runs about three times faster than one of half lines (16 rows x 64 B per instruction). The
+//     16-byte chunks are XOR-swizzled across lanes so that the 16 lanes of an MFMA operand read
+//     hit 16 distinct LDS bank groups: lane' = rr*8 + (c ^ ((rr >> 1) | (h << 2))) holds row rr
+//     (0..7) of the instruction's 8-row group, 16-byte chunk c, where h is the group's half of
+//     its 16-row block.
+// The grid is persistent (one workgroup per CU, the ring fills the LDS): each workgroup walks a
+// strided list of tiles within its XCD's contiguous share of the tile space, and issues the first
+// stages of its next tile before running the epilogue of the current one, so the pipeline's
+// fill latency hides behind the epilogue stores.
 // Reference computation: _fused_moe_kernel (tinykernels.py:1589-1765), epilogues as in the
 // weight-streaming kernels (SwiGLU with the reference's bf16 rounding points; routing-weight
 // scaling and scatter to assignment order).
@@ -25,15 +31,10 @@ namespace {
 
 typedef __attribute__((address_space(3))) void lds_void;
 
-__device__ __forceinline__ float swiglu_tile(float g, float u) {
-    g = round_bf16(g);
-    u = round_bf16(u);
-    const float s = round_bf16(g / (1.0f + __expf(-g)));
-    return s * u;
-}
-
 // s_waitcnt with only the vector-memory counter constrained (gfx9 encoding: vmcnt in bits 3:0
-// and 15:14, expcnt 6:4 and lgkmcnt 11:8 left at their maxima).
+// and 15:14, expcnt 6:4 and lgkmcnt 11:8 left at their maxima). vmcnt also counts stores; loads
+// retire in issue order, so "at most N outstanding" implies that every load but the last N
+// issued has landed.
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
     static_assert(N >= 0 && N < 64, "vmcnt range");
@@ -54,115 +55,148 @@ __device__ __forceinline__ void barrier_after_lds_reads() {
 }
 
 constexpr int kBN = 256;     // B rows per tile
-constexpr int kBlk = 1024;   // bytes per 16x32 operand block
+constexpr int kBlk = 1024;   // bytes per load instruction (and per 16x32 operand block)
+constexpr int kNW = 8;       // wavefronts per workgroup
 
+// swizzle of the 16-byte chunks of row rr in half h of a 16-row block
+__device__ __forceinline__ int a_swz(int rr, int h) { return (rr >> 1) | (h << 2); }
 
-// kStageK: MFMA k-steps (of 32) per pipeline stage; kStages: LDS ring depth (kStages - 1 stages
-// of loads in flight while one is consumed); NW: wavefronts (2 x NW/2 grid over the tile).
-template <int BM, bool GATEUP, int kStageK, int kStages, int NW>
-__global__ __launch_bounds__(64 * NW, 2) void moe_tile_kernel(GemmArgs p) {
-    constexpr int NT = 64 * NW;
-    constexpr int WN = NW / 2;              // wavefront columns
-    constexpr int MB = BM / 16;             // A row blocks per tile
+// Interleave the next k-step's LDS reads (NR) with this k-step's MFMAs (NM) in the instruction
+// stream, so that each wavefront keeps the matrix core busy while its operand reads are in
+// flight (wavefronts reach the stage barrier together, so overlap across wavefronts alone leaves
+// the LDS-bound and MFMA-bound phases of a stage serialised).
+template <int NR, int NM>
+__device__ __forceinline__ void interleave_reads_mfma() {
+    // One MFMA leads each read, and the region ends with MFMAs only: the conservative
+    // lgkmcnt(0) the compiler places before a region's first MFMA then finds the previous
+    // region's reads long landed instead of waiting on a read issued just before it.
+    static_assert(NM > NR, "more MFMAs than reads per k-step");
+#pragma unroll
+    for (int i = 0; i < NR; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one DS read
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, NM - NR, 0);
+}
+
+// Ring: A (gathered rows) in 2 slots, B (weights, the operand streamed from HBM) in NB slots, so
+// B runs NB - 1 stages ahead and A one stage ahead. Issue order per tile: B(0..NB-3), A(0),
+// B(NB-2), then at the barrier before stage s (s >= 1) A(s+1), B(s+NB-1). When the wavefront
+// waits for stage s, the only loads it has issued after A(s) are those of B(s+NB-2), if any.
+template <int BM, bool GATEUP, int WM, int NB>
+__global__ __launch_bounds__(64 * kNW, 1) void moe_tile_kernel(GemmArgs p) {
+    constexpr int NT = 64 * kNW;
+    constexpr int WN = kNW / WM;            // wavefront columns (WM wavefront rows)
+    constexpr int FM = BM / 16 / WM;        // A row blocks per wavefront
     constexpr int NBK = kBN / 16;           // B row blocks per tile (16)
-    constexpr int A_BLKS = MB * kStageK;    // A blocks per stage
-    constexpr int B_BLKS = NBK * kStageK;   // B blocks per stage
-    constexpr int NBLK = A_BLKS + B_BLKS;
-    constexpr int STAGE_BYTES = NBLK * kBlk;
-    constexpr int LPW = (NBLK + NW - 1) / NW;  // load slots per wavefront per stage
-    constexpr int FM = MB / 2;              // A blocks per wavefront (rows BM/2)
     constexpr int FN = NBK / WN;            // B blocks per wavefront
+    constexpr int A_INST = BM / 8;          // A load instructions per stage (8 rows x 128 B)
+    constexpr int LPA = A_INST / kNW;       // A loads per wavefront per stage
+    constexpr int LPB = 2 * NBK / kNW;      // B loads per wavefront per stage (4)
+    constexpr int A_BYTES = A_INST * kBlk;
+    constexpr int B_BYTES = 2 * NBK * kBlk;
+    constexpr int LB = NB - 1;              // B lookahead in stages
+    constexpr int NR = FM + FN;             // LDS reads per k-step
+    constexpr int NM = FM * FN;             // MFMAs per k-step
+    static_assert(A_INST % kNW == 0 && LPA >= 1, "A loads must split evenly over the wavefronts");
+    static_assert(LB >= 2, "B must run at least two stages ahead (wait accounting)");
     static_assert(!GATEUP || FN % 2 == 0, "gate/up block pairs per wavefront");
+    static_assert(FM * 16 * WM == BM && FN * WN == NBK, "wavefront grid must cover the tile");
+    static_assert(2 * A_BYTES + NB * B_BYTES <= 160 * 1024, "LDS budget");
     extern __shared__ __attribute__((aligned(1024))) char lds[];
 
-    const int G = p.m_tiles * p.n_tiles;
-    const int pid = blockIdx.x;
-    const int xcd = pid & 7, q8 = G >> 3, r8 = G & 7;
-    const int logical = xcd * q8 + min(xcd, r8) + (pid >> 3);
-    const int m_tile = logical % p.m_tiles, n_tile = logical / p.m_tiles;
-    const int m0 = m_tile * BM;
-    if (m0 >= p.total[0]) return;
-    const int expert = p.expert_ids[m_tile];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / WN, wn = wave % WN;
+    const int KS = p.K / 32;                // k-steps
+    const int NST = p.K / 64;               // stages
     const int OUTC = GATEUP ? kBN / 2 : kBN;
 
-    if (expert < 0) {
-        if (!GATEUP) {
-            for (int idx = tid; idx < BM * (OUTC / 8); idx += NT) {
-                const int row = idx / (OUTC / 8), cc = idx % (OUTC / 8);
-                const int flat = p.sorted_ids[m0 + row];
-                if (flat < p.numel)
-                    *reinterpret_cast<u32x4*>(p.C + (int64_t)flat * p.N + n_tile * OUTC +
-                                              cc * 8) = u32x4{0u, 0u, 0u, 0u};
-            }
-        }
-        return;
-    }
+    // Tiles that hold rows: the align step fills total[0] padded rows.
+    const int valid_m = min((p.total[0] + BM - 1) / BM, p.m_tiles);
+    const int G = valid_m * p.n_tiles;
+    const int xcd = blockIdx.x & 7, per_xcd = gridDim.x >> 3, slot = blockIdx.x >> 3;
+    const int q8 = G >> 3, r8 = G & 7;
+    const int chunk_begin = xcd * q8 + min(xcd, r8);
+    const int chunk_end = chunk_begin + q8 + (xcd < r8 ? 1 : 0);
 
-    const int r = lane & 15, q = lane >> 4;
-    const int KS = p.K / 32;                 // k-steps
-    const int NST = KS / kStageK;            // stages
-
-    // Load slots: wavefront w loads blocks w, w + NW, ... of every stage (A blocks first, then B),
-    // each lane the 16 bytes it will read back from LDS. A block (row block mb, k-step kk): the
-    // lane's gathered row at column 32*kk + 8*q; B block: 16-row block nb of the packed weights.
-    const bf16_t* src[LPW];
-    int stride[LPW];   // elements per stage
+    // Load sources. A: wavefront w issues the 8-row groups w + 8j (element offsets of each lane's
+    // row and swizzled chunk). B: instruction index w + 8j is block (nb, kk) = ((w >> 1) + 4j,
+    // w & 1), so one base pointer plus j * b_jstride covers the wavefront's loads.
+    uint32_t a_src[LPA];
+    const bf16_t* b_src = nullptr;
+    int64_t b_jstride = 0;
+    int expert = -1, m0 = 0, n_tile = 0;
+    auto setup = [&](int logical) {
+        // column tiles fastest: the tiles that share an A block run side by side, and so do
+        // the row tiles of one expert that share a B panel
+        const int m_tile = logical / p.n_tiles;
+        n_tile = logical % p.n_tiles;
+        m0 = m_tile * BM;
+        expert = p.expert_ids[m_tile];
+        if (expert < 0) return;
+        const int rr = lane >> 3;
+        const int c = (lane & 7) ^ a_swz(rr, wave & 1);
 #pragma unroll
-    for (int j = 0; j < LPW; ++j) {
-        const int b = wave + j * NW;
-        src[j] = nullptr;
-        stride[j] = 0;
-        if (b < A_BLKS) {
-            const int mb = b / kStageK, kk = b % kStageK;
-            const int row = m0 + mb * 16 + r;
-            int64_t src_row;
+        for (int j = 0; j < LPA; ++j) {
+            const int row = m0 + (wave + j * kNW) * 8 + rr;
+            int src_row;
             if (GATEUP) {
                 int flat = p.sorted_ids[row];
-                if (flat >= p.numel) flat = 0;  // padding row: any valid row, result discarded
+                if (flat >= p.numel) flat = 0;  // padding row: any valid row, discarded
                 src_row = flat / p.top_k;
             } else {
                 src_row = row;
             }
-            src[j] = p.A + src_row * p.K + kk * 32 + q * 8;
-            stride[j] = kStageK * 32;
-        } else if (b < NBLK) {
-            const int nb = (b - A_BLKS) / kStageK, kk = (b - A_BLKS) % kStageK;
-            const bf16_t* Be = p.B + (int64_t)expert * (GATEUP ? 2 : 1) * p.N * p.K;
-            src[j] = Be + ((int64_t)(n_tile * NBK + nb) * KS + kk) * 512 + lane * 8;
-            stride[j] = kStageK * 512;
+            a_src[j] = (uint32_t)src_row * (uint32_t)p.K + c * 8;
         }
+        const bf16_t* Be = p.B + (int64_t)expert * (GATEUP ? 2 : 1) * p.N * p.K;
+        b_src = Be + ((int64_t)(n_tile * NBK + (wave >> 1)) * KS + (wave & 1)) * 512 + lane * 8;
+        b_jstride = (int64_t)4 * KS * 512;
+    };
+    auto issue_a = [&](int st) {
+        char* base = lds + (st & 1) * A_BYTES;
+#pragma unroll
+        for (int j = 0; j < LPA; ++j)
+            __builtin_amdgcn_global_load_lds((const void*)(p.A + a_src[j] + st * 64),
+                                             (lds_void*)(base + (wave + j * kNW) * kBlk), 16, 0,
+                                             0);
+    };
+    auto issue_b = [&](int st) {
+        char* base = lds + 2 * A_BYTES + (st % NB) * B_BYTES;
+#pragma unroll
+        for (int j = 0; j < LPB; ++j)
+            __builtin_amdgcn_global_load_lds(
+                (const void*)(b_src + j * b_jstride + (int64_t)st * 1024),
+                (lds_void*)(base + (wave + j * kNW) * kBlk), 16, 0, 0);
+    };
+    auto prologue = [&]() {
+#pragma unroll
+        for (int s = 0; s + 1 < LB; ++s)
+            if (s < NST) issue_b(s);
+        issue_a(0);
+        if (LB - 1 < NST) issue_b(LB - 1);
+    };
+
+    // LDS byte offsets this lane reads: A block (mb, kk) at mb*2048 + a_off[kk] within an A slot;
+    // B block (nb, kk) at (nb*2 + kk) * 1024 + lane*16 within a B slot.
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void*)lds;
+    uint32_t a_off[2];
+    {
+        const int r = lane & 15, q = lane >> 4, h = r >> 3, rr = r & 7;
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk)
+            a_off[kk] = h * kBlk + (rr * 8 + ((kk * 4 + q) ^ a_swz(rr, h))) * 16;
     }
-    auto issue = [&](int st) {
-        char* base = lds + (st % kStages) * STAGE_BYTES;
-#pragma unroll
-        for (int j = 0; j < LPW; ++j) {
-            const int b = wave + j * NW;
-            if (NBLK % NW == 0 || b < NBLK)
-                __builtin_amdgcn_global_load_lds((const void*)(src[j] + (int64_t)st * stride[j]),
-                                                 (lds_void*)(base + b * kBlk), 16, 0, 0);
-        }
-    };
-    // LDS slot of A block (mb, kk): mb*kStageK + kk; of B block (nb, kk): A_BLKS + nb*kStageK+kk
-
-    const int wm = wave / WN, wn = wave % WN;
-    f32x4 acc[FM][FN];
-#pragma unroll
-    for (int f = 0; f < FM; ++f)
-#pragma unroll
-        for (int g = 0; g < FN; ++g) acc[f][g] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    const uint32_t lds_lane =
-        (uint32_t)(uintptr_t)(lds_void*)lds + (uint32_t)lane * 16;  // LDS byte address
     auto read_frags = [&](int st, int kk, u32x4 (&af)[FM], u32x4 (&bfr)[FN]) {
-        const uint32_t base = lds_lane + (st % kStages) * STAGE_BYTES;
+        const uint32_t ab = lds0 + (st & 1) * A_BYTES + a_off[kk];
+        const uint32_t bb = lds0 + 2 * A_BYTES + (st % NB) * B_BYTES + kk * kBlk + lane * 16;
 #pragma unroll
-        for (int f = 0; f < FM; ++f)
-            af[f] = lds_read16(base + ((wm * FM + f) * kStageK + kk) * kBlk);
+        for (int f = 0; f < FM; ++f) af[f] = lds_read16(ab + (wm * FM + f) * 2 * kBlk);
 #pragma unroll
-        for (int g = 0; g < FN; ++g)
-            bfr[g] = lds_read16(base + (A_BLKS + (wn * FN + g) * kStageK + kk) * kBlk);
+        for (int g = 0; g < FN; ++g) bfr[g] = lds_read16(bb + (wn * FN + g) * 2 * kBlk);
     };
+
+    f32x4 acc[FM][FN];
     auto mfmas = [&](const u32x4 (&af)[FM], const u32x4 (&bfr)[FN]) {
 #pragma unroll
         for (int f = 0; f < FM; ++f)
@@ -172,77 +206,142 @@ __global__ __launch_bounds__(64 * NW, 2) void moe_tile_kernel(GemmArgs p) {
                     as_bf16x8(af[f]), as_bf16x8(bfr[g]), acc[f][g], 0, 0, 0);
     };
 
-    // Loads issued per wavefront per stage (slots beyond NBLK issue nothing).
-    constexpr int LPS = (NBLK % NW == 0) ? LPW : -1;
-    static_assert(LPS > 0, "stage blocks must split evenly over the wavefronts");
-    constexpr int NPRE = kStages - 1;              // stages in flight ahead of the one read
+    int tile = chunk_begin + slot;
+    bool pending = false;  // the prologue loads of `tile` are already in flight
+    while (tile < chunk_end) {
+        if (!pending) {
+            setup(tile);
+            if (expert >= 0) prologue();
+        }
+        pending = false;
+        const int cur_m0 = m0, cur_n = n_tile, cur_expert = expert;
+        const int next = tile + per_xcd;
+
+        if (cur_expert < 0) {
+            // rows routed to experts outside this rank's map: down writes zeros, gate_up nothing
+            if (!GATEUP) {
+                for (int idx = tid; idx < BM * (OUTC / 8); idx += NT) {
+                    const int row = idx / (OUTC / 8), cc = idx % (OUTC / 8);
+                    const int flat = p.sorted_ids[cur_m0 + row];
+                    if (flat < p.numel)
+                        *reinterpret_cast<u32x4*>(p.C + (int64_t)flat * p.N + cur_n * OUTC +
+                                                  cc * 8) = u32x4{0u, 0u, 0u, 0u};
+                }
+            }
+            tile = next;
+            continue;
+        }
+
 #pragma unroll
-    for (int st = 0; st < NPRE; ++st)
-        if (st < NST) issue(st);
-    for (int st = 0; st < NST; ++st) {
-        // this wavefront's loads for stage st are done once only the later stages it has issued
-        // are pending; the barrier then publishes every wavefront's share of stage st and
-        // retires the reads of st - 1, whose slot the next issue overwrites
-        const int later = min(NPRE - 1, NST - 1 - st);
-        if (later >= NPRE - 1) wait_vmcnt<LPS * (NPRE - 1)>();
-        else if (NPRE >= 3 && later == 1) wait_vmcnt<LPS>();
-        else if (NPRE >= 4 && later == 2) wait_vmcnt<(NPRE >= 4 ? LPS * 2 : 0)>();
-        else if (NPRE >= 5 && later == 3) wait_vmcnt<(NPRE >= 5 ? LPS * 3 : 0)>();
+        for (int f = 0; f < FM; ++f)
+#pragma unroll
+            for (int g = 0; g < FN; ++g) acc[f][g] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+        // stage 0 published: only B(LB-1) may still be pending after A(0)
+        if (LB - 1 < NST) wait_vmcnt<LPB>();
         else wait_vmcnt<0>();
         barrier_after_lds_reads();
-        if (st + NPRE < NST) issue(st + NPRE);
-#pragma unroll
-        for (int kk = 0; kk < kStageK; ++kk) {
-            u32x4 af[FM], bfr[FN];
-            read_frags(st, kk, af, bfr);
-            mfmas(af, bfr);
-        }
-    }
+        if (1 < NST) issue_a(1);
+        if (LB < NST) issue_b(LB);
+        u32x4 a0[FM], b0[FN], a1[FM], b1[FN];
+        read_frags(0, 0, a0, b0);
 
-    // Epilogue: element i of block (f, g) is row (lane/16)*4 + i, column lane%16.
-#pragma unroll
-    for (int f = 0; f < FM; ++f) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int row = m0 + (wm * FM + f) * 16 + (lane >> 4) * 4 + i;
-            if (GATEUP) {
-                // packed w13 interleaves gate block j (2j) with up block j (2j+1)
-#pragma unroll
-                for (int pp = 0; pp < FN / 2; ++pp) {
-                    const int col = (n_tile * (NBK / 2) + wn * (FN / 2) + pp) * 16 + (lane & 15);
-                    p.C[(int64_t)row * p.N + col] =
-                        f32_to_bf16(swiglu_tile(acc[f][2 * pp][i], acc[f][2 * pp + 1][i]));
-                }
+        for (int st = 0; st < NST; ++st) {
+            read_frags(st, 1, a1, b1);
+            mfmas(a0, b0);
+            interleave_reads_mfma<NR, NM>();
+            if (st + 1 < NST) {
+                // stage st+1 published: after A(st+1) only B(st+LB) may be pending; the barrier
+                // also retires every wavefront's reads of stage st, whose slots the next loads take
+                if (st + LB < NST) wait_vmcnt<LPB>();
+                else wait_vmcnt<0>();
+                barrier_after_lds_reads();
+                if (st + 2 < NST) issue_a(st + 2);
+                if (st + 1 + LB < NST) issue_b(st + 1 + LB);
+                read_frags(st + 1, 0, a0, b0);
+                mfmas(a1, b1);
+                interleave_reads_mfma<NR, NM>();
             } else {
-                const int flat = p.sorted_ids[row];
-                if (flat < p.numel) {
-                    const float w = p.topk_w[flat];
+                mfmas(a1, b1);
+            }
+        }
+
+        // Every wavefront is done reading the ring: start the next tile's loads, then store.
+        barrier_after_lds_reads();
+        if (next < chunk_end) {
+            setup(next);
+            if (expert >= 0) prologue();
+            pending = true;
+        }
+
+        // Epilogue: element i of block (f, g) is row (lane/16)*4 + i, column lane%16.
 #pragma unroll
-                    for (int g = 0; g < FN; ++g) {
-                        const int col = (n_tile * NBK + wn * FN + g) * 16 + (lane & 15);
-                        p.C[(int64_t)flat * p.N + col] = f32_to_bf16(acc[f][g][i] * w);
+        for (int f = 0; f < FM; ++f) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int row = cur_m0 + (wm * FM + f) * 16 + (lane >> 4) * 4 + i;
+                if (GATEUP) {
+                    // packed w13 interleaves gate block j (2j) with up block j (2j+1)
+#pragma unroll
+                    for (int pp = 0; pp < FN / 2; ++pp) {
+                        const int col =
+                            (cur_n * (NBK / 2) + wn * (FN / 2) + pp) * 16 + (lane & 15);
+                        p.C[(int64_t)row * p.N + col] =
+                            f32_to_bf16(swiglu_bf16(acc[f][2 * pp][i], acc[f][2 * pp + 1][i]));
+                    }
+                } else {
+                    const int flat = p.sorted_ids[row];
+                    if (flat < p.numel) {
+                        const float w = p.topk_w[flat];
+#pragma unroll
+                        for (int g = 0; g < FN; ++g) {
+                            const int col = (cur_n * NBK + wn * FN + g) * 16 + (lane & 15);
+                            p.C[(int64_t)flat * p.N + col] = f32_to_bf16(acc[f][g][i] * w);
+                        }
                     }
                 }
             }
         }
+        tile = next;
     }
+    // A prefetched tile is always consumed (`pending` is set only for the tile visited next), so
+    // nothing is in flight here; the wait is a guard before the LDS is released.
+    wait_vmcnt<0>();
+}
+
+int cu_count() {
+    static int cus = 0;
+    if (cus == 0) {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+            n > 0)
+            cus = n;
+        else
+            cus = 256;
+    }
+    return cus;
 }
 
 template <int BM, bool GATEUP>
 void launch_tile(GemmArgs g, hipStream_t stream) {
-    constexpr int NW = BM >= 128 ? 8 : 4;                       // wavefronts per workgroup
-    constexpr int SK = ((BM / 16 + kBN / 16) % NW == 0) ? 1 : 2;  // k-steps per stage
-    constexpr int stage = (BM / 16 + kBN / 16) * SK * kBlk;     // bytes per stage
-    constexpr int NS = (80 * 1024) / stage > 6 ? 6 : (80 * 1024) / stage;  // ring depth, 2 WG/CU
-    const size_t lds = (size_t)NS * stage;
+    constexpr int WM = BM >= 128 ? 2 : 1;
+    constexpr int a_bytes = BM / 8 * kBlk, b_bytes = 2 * (kBN / 16) * kBlk;
+    constexpr int NB = (160 * 1024 - 2 * a_bytes) / b_bytes > 4 ? 4
+                                                                 : (160 * 1024 - 2 * a_bytes) / b_bytes;
+    const size_t lds = (size_t)2 * a_bytes + (size_t)NB * b_bytes;
     static bool configured = false;
     if (!configured) {
-        (void)hipFuncSetAttribute((const void*)moe_tile_kernel<BM, GATEUP, SK, NS, NW>,
+        (void)hipFuncSetAttribute((const void*)moe_tile_kernel<BM, GATEUP, WM, NB>,
                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         configured = true;
     }
-    hipLaunchKernelGGL((moe_tile_kernel<BM, GATEUP, SK, NS, NW>), dim3(g.m_tiles * g.n_tiles),
-                       dim3(64 * NW), lds, stream, g);
+    // persistent: at most one workgroup per CU, a multiple of 8 so every XCD gets the same count
+    const int64_t tiles = (int64_t)g.m_tiles * g.n_tiles;
+    int64_t grid = tiles < cu_count() ? tiles : cu_count();
+    grid = (grid + 7) / 8 * 8;
+    hipLaunchKernelGGL((moe_tile_kernel<BM, GATEUP, WM, NB>), dim3((unsigned)grid),
+                       dim3(64 * kNW), lds, stream, g);
 }
 
 }  // namespace
