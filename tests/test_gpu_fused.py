@@ -258,13 +258,14 @@ def test_packed_expert_parallel_and_tiny(dev, tsm, qwen_layer):
     p13, p2 = tsm.pack_moe_weights(w13, w2)
     emap = torch.arange(128, dtype=torch.int64, device=dev)
     emap[::2] = -1
-    for T in (50, 700):  # weight-streaming and 128-row tile kernels
+    for T in (50, 700, 3200):  # weight-streaming, 128-row and 256-row tile kernels
         x = xrand(T, 2048, dev, 77)
         w, ids, _ = tsm.moe_router(x, gw, 8, True, emap)
         out = tsm.fused_moe_packed(x, p13, p2, w, ids)
         assert torch.equal(out, tsm.fused_moe(x, w13, w2, w, ids)), f"packed EP T={T}"
-        ref = moe_reference(x.cpu(), w13c, w2c, w.cpu(), ids.cpu().long())
-        assert_close(out, ref, f"packed EP T={T}")
+        if T <= 700:  # the CPU reference is slow beyond this; above it the bit-exact match with
+            ref = moe_reference(x.cpu(), w13c, w2c, w.cpu(), ids.cpu().long())  # the layout
+            assert_close(out, ref, f"packed EP T={T}")  # checked at T=700 carries parity
     from oracle.moe_oracle import make_layer
     x, gw, w13, w2 = make_layer(37, 256, 8, 512, torch.bfloat16, seed=0, device=dev)
     p13, p2 = tsm.pack_moe_weights(w13, w2)

@@ -50,6 +50,21 @@ __device__ __forceinline__ void wait_vmcnt() {
 __device__ __forceinline__ u32x4 lds_read16(uint32_t addr) {
     return *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(addr);
 }
+__device__ __forceinline__ void lds_write2(uint32_t addr, bf16_t v) {
+    *reinterpret_cast<__attribute__((address_space(3))) bf16_t*>(addr) = v;
+}
+// Copies a loaded value into a fresh register: the compiler places its wait for the load here,
+// where nothing else is in flight, instead of at a later use behind the next tile's loads.
+__device__ __forceinline__ int settle(int v) {
+    int r;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(r) : "v"(v));
+    return r;
+}
+__device__ __forceinline__ float settle(float v) {
+    float r;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(r) : "v"(v));
+    return r;
+}
 __device__ __forceinline__ void barrier_after_lds_reads() {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
@@ -103,6 +118,15 @@ __global__ __launch_bounds__(64 * kNW, 1) void moe_tile_kernel(GemmArgs p) {
     static_assert(!GATEUP || FN % 2 == 0, "gate/up block pairs per wavefront");
     static_assert(FM * 16 * WM == BM && FN * WN == NBK, "wavefront grid must cover the tile");
     static_assert(2 * A_BYTES + NB * B_BYTES <= 160 * 1024, "LDS budget");
+    // Epilogue staging: C rows go through B slot NB-1 (the next tile's prologue fills only
+    // slots 0..NB-2), RP rows per pass, then leave as 16-byte row chunks.
+    constexpr int OUTC_C = GATEUP ? kBN / 2 : kBN;   // C columns per tile
+    constexpr int ROWB = OUTC_C * 2;                 // bytes per staged row
+    constexpr int RP = B_BYTES / ROWB < BM ? B_BYTES / ROWB : BM;
+    constexpr int NPASS = BM / RP;
+    constexpr int CPR = ROWB / 16;                   // 16-byte chunks per row
+    constexpr int CPL = RP * CPR / NT;               // chunks per lane per pass
+    static_assert(RP * CPR % NT == 0 && BM % RP == 0, "epilogue passes");
     extern __shared__ __attribute__((aligned(1024))) char lds[];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -126,26 +150,56 @@ __global__ __launch_bounds__(64 * kNW, 1) void moe_tile_kernel(GemmArgs p) {
     const bf16_t* b_src = nullptr;
     int64_t b_jstride = 0;
     int expert = -1, m0 = 0, n_tile = 0;
-    auto setup = [&](int logical) {
+    // down: assignment of tile row `tid` (tid < BM), loaded with the tile's other setup reads
+    int row_flat = 0;
+    // Tile setup in two halves: fetch() issues the reads a tile's loads depend on (its expert,
+    // and the assignment of the rows this lane gathers (gate_up) or of row `tid` (down)); for
+    // the next tile they are issued at the top of the current one, so their latency hides behind
+    // its stages, and settled after its last stage, when nothing else is in flight. finish()
+    // turns them into load sources.
+    int f_m0 = 0, f_n = 0, f_expert = -1, f_rowflat = 0;
+    int f_flat[LPA];
+    auto fetch = [&](int logical) {
         // column tiles fastest: the tiles that share an A block run side by side, and so do
         // the row tiles of one expert that share a B panel
         const int m_tile = logical / p.n_tiles;
-        n_tile = logical % p.n_tiles;
-        m0 = m_tile * BM;
-        expert = p.expert_ids[m_tile];
+        f_n = logical % p.n_tiles;
+        f_m0 = m_tile * BM;
+        f_expert = p.expert_ids[m_tile];
+        if (GATEUP) {
+#pragma unroll
+            for (int j = 0; j < LPA; ++j)
+                f_flat[j] = p.sorted_ids[f_m0 + (wave + j * kNW) * 8 + (lane >> 3)];
+        } else {
+            f_rowflat = tid < BM ? p.sorted_ids[f_m0 + tid] : (int)p.numel;
+        }
+    };
+    auto settle_fetch = [&]() {
+        f_expert = settle(f_expert);
+        if (GATEUP) {
+#pragma unroll
+            for (int j = 0; j < LPA; ++j) f_flat[j] = settle(f_flat[j]);
+        } else {
+            f_rowflat = settle(f_rowflat);
+        }
+    };
+    auto finish = [&]() {
+        m0 = f_m0;
+        n_tile = f_n;
+        expert = __builtin_amdgcn_readfirstlane(f_expert);
+        row_flat = f_rowflat;
         if (expert < 0) return;
         const int rr = lane >> 3;
         const int c = (lane & 7) ^ a_swz(rr, wave & 1);
 #pragma unroll
         for (int j = 0; j < LPA; ++j) {
-            const int row = m0 + (wave + j * kNW) * 8 + rr;
             int src_row;
             if (GATEUP) {
-                int flat = p.sorted_ids[row];
+                int flat = f_flat[j];
                 if (flat >= p.numel) flat = 0;  // padding row: any valid row, discarded
                 src_row = flat / p.top_k;
             } else {
-                src_row = row;
+                src_row = m0 + (wave + j * kNW) * 8 + rr;
             }
             a_src[j] = (uint32_t)src_row * (uint32_t)p.K + c * 8;
         }
@@ -210,11 +264,14 @@ __global__ __launch_bounds__(64 * kNW, 1) void moe_tile_kernel(GemmArgs p) {
     bool pending = false;  // the prologue loads of `tile` are already in flight
     while (tile < chunk_end) {
         if (!pending) {
-            setup(tile);
+            fetch(tile);
+            settle_fetch();
+            finish();
             if (expert >= 0) prologue();
         }
         pending = false;
         const int cur_m0 = m0, cur_n = n_tile, cur_expert = expert;
+        const int cur_flat = row_flat;
         const int next = tile + per_xcd;
 
         if (cur_expert < 0) {
@@ -237,70 +294,133 @@ __global__ __launch_bounds__(64 * kNW, 1) void moe_tile_kernel(GemmArgs p) {
 #pragma unroll
             for (int g = 0; g < FN; ++g) acc[f][g] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+        // A 256-row tile whose second half is all padding (an expert's last rows) runs as a
+        // half tile: the wavefronts of the second half keep loading and synchronising but do no
+        // LDS reads, MFMAs or stores, so each SIMD runs the first-half wavefront alone.
+        // Padding rows sit at the end of each expert's segment, so one lookup decides.
+        bool active = true;
+        if (BM == 256 && wm == 1) active = p.sorted_ids[cur_m0 + 128] < p.numel;
+
+        // Stage pipeline bookkeeping shared by both loops: stage st+1 published (after A(st+1)
+        // only B(st+LB) may be pending); the barrier also retires every wavefront's reads of
+        // stage st, whose slots the next loads take.
+        auto advance = [&](int st) {
+            if (st + LB < NST) wait_vmcnt<LPB>();
+            else wait_vmcnt<0>();
+            barrier_after_lds_reads();
+            if (st + 2 < NST) issue_a(st + 2);
+            if (st + 1 + LB < NST) issue_b(st + 1 + LB);
+        };
+
         // stage 0 published: only B(LB-1) may still be pending after A(0)
         if (LB - 1 < NST) wait_vmcnt<LPB>();
         else wait_vmcnt<0>();
         barrier_after_lds_reads();
+        // down: the routing weight of row `tid`, loaded here (older than every load of the
+        // stages below, so their vmcnt accounting is unchanged) and settled after the last stage
+        float row_w = 0.0f;
+        if (!GATEUP && tid < BM) row_w = p.topk_w[cur_flat < p.numel ? cur_flat : 0];
+        if (next < chunk_end) fetch(next);
         if (1 < NST) issue_a(1);
         if (LB < NST) issue_b(LB);
-        u32x4 a0[FM], b0[FN], a1[FM], b1[FN];
-        read_frags(0, 0, a0, b0);
-
-        for (int st = 0; st < NST; ++st) {
-            read_frags(st, 1, a1, b1);
-            mfmas(a0, b0);
-            interleave_reads_mfma<NR, NM>();
-            if (st + 1 < NST) {
-                // stage st+1 published: after A(st+1) only B(st+LB) may be pending; the barrier
-                // also retires every wavefront's reads of stage st, whose slots the next loads take
-                if (st + LB < NST) wait_vmcnt<LPB>();
-                else wait_vmcnt<0>();
-                barrier_after_lds_reads();
-                if (st + 2 < NST) issue_a(st + 2);
-                if (st + 1 + LB < NST) issue_b(st + 1 + LB);
+        if (active) {
+            u32x4 a0[FM], b0[FN], a1[FM], b1[FN];
+            read_frags(0, 0, a0, b0);
+            // One straight-line body per stage (no path split around the last stage) keeps the
+            // accumulators in place across iterations; the last stage's read of "stage NST" only
+            // touches ring slots no load is writing at that point, and its values are unused.
+            for (int st = 0; st < NST; ++st) {
+                read_frags(st, 1, a1, b1);
+                mfmas(a0, b0);
+                interleave_reads_mfma<NR, NM>();
+                if (st + 1 < NST) advance(st);
                 read_frags(st + 1, 0, a0, b0);
                 mfmas(a1, b1);
                 interleave_reads_mfma<NR, NM>();
-            } else {
-                mfmas(a1, b1);
             }
+        } else {
+            for (int st = 0; st + 1 < NST; ++st) advance(st);
         }
 
+        if (!GATEUP) row_w = settle(cur_flat < p.numel ? row_w : 0.0f);
+        if (next < chunk_end) settle_fetch();
         // Every wavefront is done reading the ring: start the next tile's loads, then store.
         barrier_after_lds_reads();
         if (next < chunk_end) {
-            setup(next);
+            finish();
             if (expert >= 0) prologue();
             pending = true;
         }
 
-        // Epilogue: element i of block (f, g) is row (lane/16)*4 + i, column lane%16.
+        // Epilogue, NPASS passes of RP rows through the staging slot: the owners of the pass's
+        // rows write them (element i of block (f, g) is row (lane/16)*4 + i, column lane%16;
+        // 16-byte chunks XOR-swizzled by row so the four row groups of a write hit different
+        // banks), then every lane stores whole 16-byte chunks of rows. Wavefronts of an inactive
+        // half tile take part in the barriers; their rows are padding and are never stored.
+        const uint32_t stage_lds = lds0 + 2 * A_BYTES + (NB - 1) * B_BYTES;
+        auto swz_c = [](int rl) { return ((rl >> 2) & 3) << 2; };
+        // down: per-row (assignment, weight) in A slot 1, which the next tile's prologue leaves
+        // alone (its A(1) load is issued after that tile's first barrier)
+        const uint32_t meta_lds = lds0 + A_BYTES;
+        if (!GATEUP) {
+            if (tid < BM) {
+                *reinterpret_cast<__attribute__((address_space(3))) int*>(meta_lds + tid * 8) = cur_flat;
+                *reinterpret_cast<__attribute__((address_space(3))) float*>(meta_lds + tid * 8 + 4) = row_w;
+            }
+            barrier_after_lds_reads();
+        }
+#pragma unroll 1
+        for (int ps = 0; ps < NPASS; ++ps) {
+            if (active) {
 #pragma unroll
-        for (int f = 0; f < FM; ++f) {
+                for (int f = 0; f < FM; ++f) {
+                    const int rb = (wm * FM + f) * 16 - ps * RP;  // block's first staged row
+                    if (rb < 0 || rb >= RP) continue;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int row = cur_m0 + (wm * FM + f) * 16 + (lane >> 4) * 4 + i;
-                if (GATEUP) {
-                    // packed w13 interleaves gate block j (2j) with up block j (2j+1)
+                    for (int i = 0; i < 4; ++i) {
+                        const int rl = rb + (lane >> 4) * 4 + i;
+                        const uint32_t rbase = stage_lds + rl * ROWB;
+                        float w = 0.0f;
+                        if (!GATEUP)
+                            w = *reinterpret_cast<const __attribute__((address_space(3))) float*>(
+                                meta_lds + (ps * RP + rl) * 8 + 4);
+                        if (GATEUP) {
+                            // packed w13 interleaves gate block j (2j) with up block j (2j+1)
 #pragma unroll
-                    for (int pp = 0; pp < FN / 2; ++pp) {
-                        const int col =
-                            (cur_n * (NBK / 2) + wn * (FN / 2) + pp) * 16 + (lane & 15);
-                        p.C[(int64_t)row * p.N + col] =
-                            f32_to_bf16(swiglu_bf16(acc[f][2 * pp][i], acc[f][2 * pp + 1][i]));
-                    }
-                } else {
-                    const int flat = p.sorted_ids[row];
-                    if (flat < p.numel) {
-                        const float w = p.topk_w[flat];
+                            for (int pp = 0; pp < FN / 2; ++pp) {
+                                const int col = (wn * (FN / 2) + pp) * 16 + (lane & 15);
+                                lds_write2(rbase + ((((col >> 3) ^ swz_c(rl)) << 4) | ((col & 7) << 1)),
+                                           f32_to_bf16(swiglu_bf16(acc[f][2 * pp][i],
+                                                                   acc[f][2 * pp + 1][i])));
+                            }
+                        } else {
 #pragma unroll
-                        for (int g = 0; g < FN; ++g) {
-                            const int col = (cur_n * NBK + wn * FN + g) * 16 + (lane & 15);
-                            p.C[(int64_t)flat * p.N + col] = f32_to_bf16(acc[f][g][i] * w);
+                            for (int g = 0; g < FN; ++g) {
+                                const int col = (wn * FN + g) * 16 + (lane & 15);
+                                lds_write2(rbase + ((((col >> 3) ^ swz_c(rl)) << 4) | ((col & 7) << 1)),
+                                           f32_to_bf16(acc[f][g][i] * w));
+                            }
                         }
                     }
                 }
             }
+            barrier_after_lds_reads();
+#pragma unroll
+            for (int k = 0; k < CPL; ++k) {
+                const int c = tid + k * NT, rl = c / CPR, j = c % CPR;
+                const u32x4 v = lds_read16(stage_lds + rl * ROWB + ((j ^ swz_c(rl)) << 4));
+                if (GATEUP) {
+                    const int row = cur_m0 + ps * RP + rl;
+                    *reinterpret_cast<u32x4*>(p.C + (int64_t)row * p.N + cur_n * OUTC_C + j * 8) = v;
+                } else {
+                    const int flat = *reinterpret_cast<const __attribute__((address_space(3))) int*>(
+                        meta_lds + (ps * RP + rl) * 8);
+                    if (flat < p.numel)
+                        *reinterpret_cast<u32x4*>(p.C + (int64_t)flat * p.N + cur_n * OUTC_C +
+                                                  j * 8) = v;
+                }
+            }
+            if (ps + 1 < NPASS) barrier_after_lds_reads();
         }
         tile = next;
     }
