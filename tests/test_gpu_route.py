@@ -104,3 +104,25 @@ def test_router_matches_torch_closed_form(dev, tsm, qwen_layer):
     tw = tw / tw.sum(-1, keepdim=True)
     assert torch.allclose(w.cpu(), tw, atol=2e-6, rtol=1e-5)
     assert bool((w[:, :-1] >= w[:, 1:]).all())
+
+
+@pytest.mark.parametrize("T", [1, 64, 256])
+@pytest.mark.parametrize("logits_bf16", [False, True])
+def test_router_single_launch_without_logits_buffer(dev, tsm, qwen_layer, T, logits_bf16):
+    """tsm_moe_router without a logits buffer (as the fused forward calls it) gives the same bits
+    as with one."""
+    from tinyserve_amd import _lib
+    print(f"router single-launch T={T} logits_bf16={logits_bf16}", flush=True)
+    (gate_w, _, _), _ = qwen_layer
+    g = torch.Generator(device=dev).manual_seed(100 + T)
+    x = torch.randn(T, 2048, generator=g, device=dev).bfloat16()
+    w, ids, _ = tsm.moe_router(x, gate_w, 8, True, None, None, logits_bf16)
+    w1 = torch.empty_like(w)
+    ids1 = torch.empty_like(ids)
+    rc = _lib.lib.tsm_moe_router(_lib.ptr(x), _lib.ptr(gate_w), 1, T, 2048, 128, 8, 1, None, None,
+                                 int(logits_bf16), None, _lib.ptr(w1), _lib.ptr(ids1),
+                                 _lib.stream_of(x))
+    _lib.check(rc, "tsm_moe_router")
+    torch.cuda.synchronize()
+    assert torch.equal(ids1, ids)
+    assert same_bits(w1.cpu().numpy(), w.cpu().numpy())

@@ -61,10 +61,49 @@ __device__ __forceinline__ float wave_sum_butterfly(float v) {
     return v;
 }
 
+// Cross-lane reductions whose result does not depend on the combination order (max, and argmax
+// under a total order) use DPP row operations instead of LDS-routed shuffles: xor 1 and xor 2
+// within quads, mirrors within 8 and 16 lanes, then the row-15 / row-31 broadcasts carry the
+// row results up to lane 63, which is read back into every lane.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_update_dpp(v, v, CTRL, ROW_MASK, 0xF, false);
+}
+
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ void max_step(float& v) {
+    v = fmaxf(v, __int_as_float(dpp_i<CTRL, ROW_MASK>(__float_as_int(v))));
+}
+
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int s = 32; s >= 1; s >>= 1) v = fmaxf(v, __shfl_xor(v, s));
-    return v;
+    max_step<0xB1, 0xF>(v);   // quad_perm [1,0,3,2]
+    max_step<0x4E, 0xF>(v);   // quad_perm [2,3,0,1]
+    max_step<0x141, 0xF>(v);  // row_half_mirror
+    max_step<0x140, 0xF>(v);  // row_mirror
+    max_step<0x142, 0xA>(v);  // row_bcast:15 into rows 1 and 3
+    max_step<0x143, 0xC>(v);  // row_bcast:31 into rows 2 and 3
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// (largest value, lowest index among equal values) over the wavefront.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ void argmax_step(float& bv, int& bi) {
+    const float ov = __int_as_float(dpp_i<CTRL, ROW_MASK>(__float_as_int(bv)));
+    const int oi = dpp_i<CTRL, ROW_MASK>(bi);
+    const bool take = ov > bv || (ov == bv && oi < bi);
+    bv = take ? ov : bv;
+    bi = take ? oi : bi;
+}
+
+__device__ __forceinline__ void wave_argmax(float& bv, int& bi) {
+    argmax_step<0xB1, 0xF>(bv, bi);
+    argmax_step<0x4E, 0xF>(bv, bi);
+    argmax_step<0x141, 0xF>(bv, bi);
+    argmax_step<0x140, 0xF>(bv, bi);
+    argmax_step<0x142, 0xA>(bv, bi);
+    argmax_step<0x143, 0xC>(bv, bi);
+    bv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bv), 63));
+    bi = __builtin_amdgcn_readlane(bi, 63);
 }
 
 // exp(x) in fp32 for the router softmax, written out with explicit fmaf so the host oracle
@@ -74,10 +113,11 @@ __device__ __forceinline__ float wave_max(float v) {
 // Inputs below -86 (including -inf and NaN) return 0, so results are never subnormal.
 __device__ __forceinline__ float router_expf(float x) {
 #pragma clang fp contract(off)
-    if (!(x >= -86.0f)) return 0.0f;
-    if (x > 88.0f) return __builtin_huge_valf();
-    float n = __builtin_rintf(x * 1.44269504088896341f);
-    float r = __builtin_fmaf(-n, 0.693145751953125f, x);
+    // branch-free: the polynomial runs on the input clamped to [-86, 88] (unchanged inside that
+    // range), and the out-of-range results are selected afterwards
+    const float xc = __builtin_fminf(__builtin_fmaxf(x, -86.0f), 88.0f);
+    float n = __builtin_rintf(xc * 1.44269504088896341f);
+    float r = __builtin_fmaf(-n, 0.693145751953125f, xc);
     r = __builtin_fmaf(-n, 1.42860682030941723e-06f, r);
     float p = 1.98412698412698413e-04f;  // 1/7!
     p = __builtin_fmaf(p, r, 1.38888888888888889e-03f);  // 1/6!
@@ -87,7 +127,8 @@ __device__ __forceinline__ float router_expf(float x) {
     p = __builtin_fmaf(p, r, 0.5f);
     p = __builtin_fmaf(p, r, 1.0f);
     p = __builtin_fmaf(p, r, 1.0f);
-    return __builtin_ldexpf(p, (int)n);
+    const float e = __builtin_ldexpf(p, (int)n);
+    return (x >= -86.0f) ? (x > 88.0f ? __builtin_huge_valf() : e) : 0.0f;
 }
 
 }  // namespace tsm

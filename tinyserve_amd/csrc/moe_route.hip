@@ -30,20 +30,21 @@ __device__ __forceinline__ void wave_select(float (&v)[kMaxM], int E, int top_k,
                                             int32_t* __restrict__ out_ids) {
 #pragma clang fp contract(off)
     const int lane = threadIdx.x & (kWave - 1);
+    const int nq = (E + 63) >> 6;  // slots in use (uniform): the loops below skip the rest
     float m = -__builtin_huge_valf();
 #pragma unroll
     for (int q = 0; q < kMaxM; ++q)
-        if (lane + 64 * q < E) m = fmaxf(m, v[q]);
+        if (q < nq && lane + 64 * q < E) m = fmaxf(m, v[q]);
     m = wave_max(m);
 
     float part = 0.0f;  // this lane's share of sum(p), ascending q
 #pragma unroll
     for (int q = 0; q < kMaxM; ++q) {
-        if (lane + 64 * q < E) {
-            v[q] = router_expf(v[q] - m);
-            part = part + v[q];
-        } else {
-            v[q] = -__builtin_huge_valf();
+        if (q < nq) {
+            const bool in = lane + 64 * q < E;
+            const float pe = router_expf(v[q] - m);
+            v[q] = in ? pe : -__builtin_huge_valf();
+            part = in ? part + pe : part;
         }
     }
 
@@ -54,18 +55,18 @@ __device__ __forceinline__ void wave_select(float (&v)[kMaxM], int E, int top_k,
         int bi = 0x7fffffff;
 #pragma unroll
         for (int q = 0; q < kMaxM; ++q)
-            if (v[q] > bv) { bv = v[q]; bi = lane + 64 * q; }
-#pragma unroll
-        for (int sh = 32; sh >= 1; sh >>= 1) {
-            float ov = __shfl_xor(bv, sh);
-            int oi = __shfl_xor(bi, sh);
-            if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
-        }
+            if (q < nq) {
+                const bool take = v[q] > bv;  // ascending q: the lowest index wins ties
+                bv = take ? v[q] : bv;
+                bi = take ? lane + 64 * q : bi;
+            }
+        wave_argmax(bv, bi);
         sel_sum = sel_sum + bv;
-        if (lane == s) { my_v = bv; my_i = bi; }
+        my_v = lane == s ? bv : my_v;
+        my_i = lane == s ? bi : my_i;
 #pragma unroll
         for (int q = 0; q < kMaxM; ++q)
-            if (bi == lane + 64 * q) v[q] = -__builtin_huge_valf();
+            if (q < nq) v[q] = bi == lane + 64 * q ? -__builtin_huge_valf() : v[q];
     }
     float denom = renorm ? sel_sum : wave_sum_butterfly(part);
     if (lane < top_k) {
