@@ -250,6 +250,59 @@ __global__ __launch_bounds__(64 * kNW, 1) void moe_tile_kernel(GemmArgs p) {
         for (int g = 0; g < FN; ++g) bfr[g] = lds_read16(bb + (wn * FN + g) * 2 * kBlk);
     };
 
+    // Tile order: each expert's tiles column-major, i.e. the row tiles that share a weight panel
+    // are adjacent in the list, so the tiles an XCD runs at once span few panels and few panels
+    // straddle two consecutive rounds (row-major order re-fetched about one expert's panels per
+    // round). The workgroup remaps its strided tile list once, at start: expert_ids goes into
+    // LDS (before the ring uses it), each lane k binary-searches the bucket of its k-th tile
+    // (expert_ids is non-decreasing with the remote bucket's -1 taken as +inf) and keeps the
+    // plain index (row tile * n_tiles + column tile). Lists longer than 128 tiles per workgroup,
+    // or tables larger than the LDS, keep the plain order.
+    int remap0 = -1, remap1 = -1;
+    constexpr int kMaxTable = 2 * A_BYTES / 4;  // both A slots
+    const bool remapped =
+        valid_m <= kMaxTable && (chunk_end - chunk_begin + per_xcd - 1) / per_xcd <= 128;
+    if (remapped) {
+        int* table = reinterpret_cast<int*>(lds);
+        for (int i = tid; i < valid_m; i += NT) {
+            const int e = p.expert_ids[i];
+            table[i] = e < 0 ? 0x7fffffff : e;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int L = chunk_begin + slot + (lane + 64 * h) * per_xcd;
+            int v = -1;
+            if (L < chunk_end) {
+                const int mt = L / p.n_tiles;
+                const int key = table[mt];
+                int lo = 0, hi = mt;  // first tile with table == key
+                while (lo < hi) {
+                    const int mid = (lo + hi) >> 1;
+                    if (table[mid] < key) lo = mid + 1;
+                    else hi = mid;
+                }
+                int lo2 = mt + 1, hi2 = valid_m;  // one past its last tile
+                while (lo2 < hi2) {
+                    const int mid = (lo2 + hi2) >> 1;
+                    if (table[mid] <= key) lo2 = mid + 1;
+                    else hi2 = mid;
+                }
+                const int first = lo, count = lo2 - lo;
+                const int local = L - first * p.n_tiles;
+                v = (first + local % count) * p.n_tiles + local / count;
+            }
+            if (h == 0) remap0 = v;
+            else remap1 = v;
+        }
+        __syncthreads();  // the table's LDS is the ring's from here on
+    }
+    auto tile_index = [&](int L) {
+        if (!remapped) return L;
+        const int k = (L - chunk_begin - slot) / per_xcd;
+        return __builtin_amdgcn_readlane(k < 64 ? remap0 : remap1, k & 63);
+    };
+
     f32x4 acc[FM][FN];
     auto mfmas = [&](const u32x4 (&af)[FM], const u32x4 (&bfr)[FN]) {
 #pragma unroll
@@ -264,7 +317,7 @@ __global__ __launch_bounds__(64 * kNW, 1) void moe_tile_kernel(GemmArgs p) {
     bool pending = false;  // the prologue loads of `tile` are already in flight
     while (tile < chunk_end) {
         if (!pending) {
-            fetch(tile);
+            fetch(tile_index(tile));
             settle_fetch();
             finish();
             if (expert >= 0) prologue();
@@ -320,7 +373,7 @@ __global__ __launch_bounds__(64 * kNW, 1) void moe_tile_kernel(GemmArgs p) {
         // stages below, so their vmcnt accounting is unchanged) and settled after the last stage
         float row_w = 0.0f;
         if (!GATEUP && tid < BM) row_w = p.topk_w[cur_flat < p.numel ? cur_flat : 0];
-        if (next < chunk_end) fetch(next);
+        if (next < chunk_end) fetch(tile_index(next));
         if (1 < NST) issue_a(1);
         if (LB < NST) issue_b(LB);
         if (active) {
