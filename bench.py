@@ -52,6 +52,54 @@ def stage_flops(T):
     return {"router": 2 * T * H * E, "gate_up": 2 * numel * H * 2 * I, "down": 2 * numel * I * H}
 
 
+def torch_moe_layer(x, gw, w13, w2, top_k=8):
+    """The same layer composed from stock PyTorch-ROCm ops on the GPU (what a framework without
+    a fused MoE kernel runs): fp32 router + softmax + top-k + renormalise, assignments sorted
+    by expert, per-expert hipBLASLt GEMMs with the reference's bf16 rounding points, weighted
+    rows added into an fp32 output. Comparison baseline only; not a parity reference."""
+    import torch
+    T, H = x.shape
+    I = w2.shape[-1]
+    p = torch.softmax(torch.nn.functional.linear(x.float(), gw.float()), dim=-1)
+    w, ids = torch.topk(p, top_k, dim=-1)
+    w = w / w.sum(-1, keepdim=True)
+    flat_ids = ids.reshape(-1)
+    order = torch.argsort(flat_ids, stable=True)
+    counts = torch.bincount(flat_ids, minlength=w13.shape[0]).tolist()
+    tok = order // top_k
+    out = torch.zeros(T, H, dtype=torch.float32, device=x.device)
+    start = 0
+    for e, c in enumerate(counts):
+        if c == 0:
+            continue
+        sel = order[start:start + c]
+        t_e = tok[start:start + c]
+        h = x[t_e] @ w13[e].t()
+        a = torch.nn.functional.silu(h[:, :I]) * h[:, I:]
+        y = (a @ w2[e].t()).float() * w.reshape(-1)[sel, None]
+        out.index_add_(0, t_e, y)
+        start += c
+    return out.to(x.dtype)
+
+
+def torch_gpu_baseline(layer, x, T, layer_b):
+    import torch
+    gw, w13, w2 = layer
+    for _ in range(3):
+        torch_moe_layer(x, gw, w13, w2)
+    torch.cuda.synchronize()
+    reps, t0 = 0, time.perf_counter()
+    while reps < 20 and (reps < 3 or time.perf_counter() - t0 < 3.0):
+        torch_moe_layer(x, gw, w13, w2)
+        reps += 1
+    torch.cuda.synchronize()
+    t = (time.perf_counter() - t0) / reps
+    return {"us_per_layer": t * 1e6, "GBps": layer_b / t / 1e9, "reps": reps,
+            "kind": "stock PyTorch-ROCm ops on the same GPU (fp32 router, sort by expert, "
+                    "per-expert hipBLASLt GEMMs, index_add into fp32); the reference's Triton "
+                    "kernels cannot run on the GPU box"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -61,6 +109,7 @@ def main():
     ap.add_argument("--layers", type=int, default=8, help="distinct layer copies cycled over")
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-torch-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 1 GiB device copy (counter calibration for rocprofv3)")
@@ -347,6 +396,9 @@ def main():
                           "n_touched": nt})
             log(json.dumps(sweep[-1]))
         res["sweep"] = sweep
+
+    if not args.no_torch_baseline:
+        res["torch_gpu_baseline"] = torch_gpu_baseline(layers[0], inputs(T, 1000 + T)[0], T, B)
 
     if not args.no_cpu_baseline:
         from oracle.moe_oracle import moe_reference, route_torch
