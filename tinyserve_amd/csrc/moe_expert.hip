@@ -26,9 +26,9 @@ constexpr int kMaxBucketsE = 513;
 
 template <int S, int NB, int WN, bool GATEUP, bool PACKED, bool SPEC>
 __global__ __launch_bounds__(256 * WN, 2) void moe_expert_kernel(ExpertArgs p) {
-    static_assert(!GATEUP || WN == 1, "gate_up uses one wavefront group");
+    static_assert(!GATEUP || NB == 2, "gate_up: one gate and one up block per wavefront group");
     constexpr int NT = 256 * WN;
-    constexpr int OUTC = GATEUP ? 16 : 16 * NB * WN;  // output columns per workgroup
+    constexpr int OUTC = GATEUP ? 16 * WN : 16 * NB * WN;  // output columns per workgroup
     __shared__ f32x4 red[4][WN * NB][64];
     __shared__ int s_hist[kMaxBucketsE];
     __shared__ int s_rows[kExpertMaxRows];
@@ -61,12 +61,12 @@ __global__ __launch_bounds__(256 * WN, 2) void moe_expert_kernel(ExpertArgs p) {
             const u32x4* src;
             int stride;
             if (PACKED) {
-                const int blk = GATEUP ? 2 * n_tile + nb : (n_tile * WN + wgrp) * NB + nb;
+                const int blk = (n_tile * WN + wgrp) * NB + nb;  // gate_up: gate 2c, up 2c+1
                 src = reinterpret_cast<const u32x4*>(
                           Be + ((int64_t)blk * (p.K / 32) + wave * S) * 512) + lane;
                 stride = 64;
             } else {
-                const int row = GATEUP ? (nb == 0 ? 0 : p.N) + n_tile * 16 + r
+                const int row = GATEUP ? (nb == 0 ? 0 : p.N) + (n_tile * WN + wgrp) * 16 + r
                                        : n_tile * OUTC + (wgrp * NB + nb) * 16 + r;
                 src = reinterpret_cast<const u32x4*>(Be + (int64_t)row * p.K + kbase);
                 stride = 4;
@@ -118,16 +118,15 @@ __global__ __launch_bounds__(256 * WN, 2) void moe_expert_kernel(ExpertArgs p) {
     __syncthreads();
     const int start = s_start;
 
-    // 3. 16-row sub-tiles of this expert's assignments
-    for (int m0 = 0; m0 < count; m0 += 16) {
+    // 3. 16-row sub-tiles of this expert's assignments. The rows of sub-tile m0 + 16 are
+    // requested right after sub-tile m0's MFMAs are issued, so their latency overlaps its
+    // reduction and epilogue (the MFMAs have read the registers the new rows land in).
+    u32x4 a[S];
+    auto load_a = [&](int m0) {
         const int j = m0 + r;
-        const bf16_t* a_src = nullptr;
         if (j < count) {
-            a_src = GATEUP ? p.A + (int64_t)(s_rows[j] / p.top_k) * p.K + kbase
-                           : p.A + (int64_t)(start + j) * p.K + kbase;
-        }
-        u32x4 a[S];
-        if (a_src) {
+            const bf16_t* a_src = GATEUP ? p.A + (int64_t)(s_rows[j] / p.top_k) * p.K + kbase
+                                         : p.A + (int64_t)(start + j) * p.K + kbase;
             const u32x4* src = reinterpret_cast<const u32x4*>(a_src);
 #pragma unroll
             for (int s = 0; s < S; ++s) a[s] = src[4 * s];
@@ -135,6 +134,9 @@ __global__ __launch_bounds__(256 * WN, 2) void moe_expert_kernel(ExpertArgs p) {
 #pragma unroll
             for (int s = 0; s < S; ++s) a[s] = u32x4{0u, 0u, 0u, 0u};
         }
+    };
+    load_a(0);
+    for (int m0 = 0; m0 < count; m0 += 16) {
         f32x4 acc[NB];
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) acc[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -145,6 +147,7 @@ __global__ __launch_bounds__(256 * WN, 2) void moe_expert_kernel(ExpertArgs p) {
                 acc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a[s]),
                                                                   as_bf16x8(b[nb][s]), acc[nb],
                                                                   0, 0, 0);
+        if (m0 + 16 < count) load_a(m0 + 16);
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) red[wave][wgrp * NB + nb][lane] = acc[nb];
         __syncthreads();
@@ -160,7 +163,7 @@ __global__ __launch_bounds__(256 * WN, 2) void moe_expert_kernel(ExpertArgs p) {
                         red[3][bb][l][i];
             }
             if (GATEUP) {
-                p.C[(int64_t)(start + m0 + row) * p.N + n_tile * 16 + col] =
+                p.C[(int64_t)(start + m0 + row) * p.N + (n_tile * WN + wgrp) * 16 + col] =
                     f32_to_bf16(swiglu_bf16(v[0], v[1]));
             } else {
                 const int flat = s_rows[m0 + row];
@@ -187,17 +190,26 @@ void launch_e(const ExpertArgs& g, hipStream_t stream) {
                            dim3(experts * g.n_tiles), dim3(256 * WN), 0, stream, g);
 }
 
-template <bool PACKED>
-bool gate_up_e(const ExpertArgs& g, hipStream_t stream) {
+// gate_up with WN wavefront groups (16 activation columns each) per workgroup.
+template <bool PACKED, int WN>
+bool gate_up_wn(ExpertArgs g, hipStream_t stream) {
+    g.n_tiles = g.N / (16 * WN);
     switch (g.K / 128) {
-        case 2: launch_e<2, 2, true, PACKED>(g, stream); return true;
-        case 4: launch_e<4, 2, true, PACKED>(g, stream); return true;
-        case 6: launch_e<6, 2, true, PACKED>(g, stream); return true;
-        case 8: launch_e<8, 2, true, PACKED>(g, stream); return true;
-        case 12: launch_e<12, 2, true, PACKED>(g, stream); return true;
-        case 16: launch_e<16, 2, true, PACKED>(g, stream); return true;
+        case 2: launch_e<2, 2, true, PACKED, WN>(g, stream); return true;
+        case 4: launch_e<4, 2, true, PACKED, WN>(g, stream); return true;
+        case 6: launch_e<6, 2, true, PACKED, WN>(g, stream); return true;
+        case 8: launch_e<8, 2, true, PACKED, WN>(g, stream); return true;
+        case 12: launch_e<12, 2, true, PACKED, WN>(g, stream); return true;
+        case 16: launch_e<16, 2, true, PACKED, WN>(g, stream); return true;
         default: return false;
     }
+}
+
+template <bool PACKED>
+bool gate_up_e(const ExpertArgs& g, hipStream_t stream) {
+    // one wavefront group: two (8 waves at ~210 VGPRs, one workgroup per CU) measured slower
+    // at every batch size although they halve the gathered x reads
+    return gate_up_wn<PACKED, 1>(g, stream);
 }
 
 template <bool PACKED>
@@ -237,7 +249,6 @@ bool expert_path_supported(int64_t numel, int H, int I, int E) {
 
 bool launch_expert_gate_up(ExpertArgs g, bool packed, hipStream_t stream) {
     if (g.N % 16 != 0 || g.K % 128 != 0) return false;
-    g.n_tiles = g.N / 16;
     return packed ? gate_up_e<true>(g, stream) : gate_up_e<false>(g, stream);
 }
 
