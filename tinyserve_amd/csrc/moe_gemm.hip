@@ -203,6 +203,9 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(GemmArgs p) {
 }
 
 // out[t, :] = bf16(sum over s = 0..k-1 of rows[t*k + s, :]) with fp32 accumulation in slot order.
+// STREAM: rows larger than the L2s are read and the output written with non-temporal accesses;
+// smaller rows were just written by the down GEMM and are read from L2.
+template <bool STREAM>
 __global__ __launch_bounds__(256) void combine_kernel(const bf16_t* __restrict__ rows,
                                                       bf16_t* __restrict__ out, int64_t T, int H,
                                                       int k) {
@@ -213,7 +216,8 @@ __global__ __launch_bounds__(256) void combine_kernel(const bf16_t* __restrict__
     if (t >= T) return;
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     for (int s = 0; s < k; ++s) {
-        const u32x4 v = *reinterpret_cast<const u32x4*>(rows + ((t * k + s) * H + c * 8));
+        const u32x4* src = reinterpret_cast<const u32x4*>(rows + ((t * k + s) * H + c * 8));
+        const u32x4 v = STREAM ? __builtin_nontemporal_load(src) : *src;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             acc[2 * j] += lo_bf16(v[j]);
@@ -223,7 +227,9 @@ __global__ __launch_bounds__(256) void combine_kernel(const bf16_t* __restrict__
     u32x4 o;
 #pragma unroll
     for (int j = 0; j < 4; ++j) o[j] = pack_bf16(acc[2 * j], acc[2 * j + 1]);
-    *reinterpret_cast<u32x4*>(out + (t * H + c * 8)) = o;
+    u32x4* dst = reinterpret_cast<u32x4*>(out + (t * H + c * 8));
+    if (STREAM) __builtin_nontemporal_store(o, dst);
+    else *dst = o;
 }
 
 __global__ __launch_bounds__(256) void silu_mul_kernel(const bf16_t* __restrict__ gate,
@@ -376,8 +382,13 @@ void launch_down(const bf16_t* act, const bf16_t* w2, const float* topk_w, const
 void launch_combine(const bf16_t* rows, int64_t T, int H, int top_k, bf16_t* out,
                     hipStream_t stream) {
     const int64_t threads = T * (H / 8);
-    hipLaunchKernelGGL(combine_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
-                       stream, rows, out, T, H, top_k);
+    const dim3 grid((unsigned)((threads + 255) / 256));
+    if ((int64_t)T * top_k * H * 2 > (32ll << 20))  // beyond the combined L2 of the 8 XCDs
+        hipLaunchKernelGGL(combine_kernel<true>, grid, dim3(256), 0, stream, rows, out, T, H,
+                           top_k);
+    else
+        hipLaunchKernelGGL(combine_kernel<false>, grid, dim3(256), 0, stream, rows, out, T, H,
+                           top_k);
 }
 
 ExpertArgs expert_args(const bf16_t* A, const bf16_t* B, bf16_t* C, const float* topk_w,
