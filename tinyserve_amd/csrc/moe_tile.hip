@@ -468,9 +468,11 @@ __global__ __launch_bounds__(64 * kNW, 1) void moe_tile_kernel(GemmArgs p) {
                 } else {
                     const int flat = *reinterpret_cast<const __attribute__((address_space(3))) int*>(
                         meta_lds + (ps * RP + rl) * 8);
+                    // the rows are read once, by the k-sum, after this kernel: non-temporal
                     if (flat < p.numel)
-                        *reinterpret_cast<u32x4*>(p.C + (int64_t)flat * p.N + cur_n * OUTC_C +
-                                                  j * 8) = v;
+                        __builtin_nontemporal_store(
+                            v, reinterpret_cast<u32x4*>(p.C + (int64_t)flat * p.N +
+                                                         cur_n * OUTC_C + j * 8));
                 }
             }
             if (ps + 1 < NPASS) barrier_after_lds_reads();
