@@ -269,17 +269,23 @@ __global__ __launch_bounds__(kTileWaves * 64) void router_tile_kernel(
 #pragma clang fp contract(off)
     constexpr int W = NC * 512;
     constexpr int EPC = 16 / sizeof(TIn);
-    __shared__ __attribute__((aligned(16))) TIn s_x[kTT * W];
+    // x rows converted to fp32 once here, so the inner loop does no conversions for them
+    __shared__ __attribute__((aligned(16))) float s_x[kTT * W];
     __shared__ float s_logits[kTT * 512];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int64_t t0 = (int64_t)blockIdx.x * kTT;
 
-    for (int idx = threadIdx.x; idx < kTT * W / EPC; idx += kTileWaves * 64) {
-        const int tb = idx / (W / EPC), h = (idx % (W / EPC)) * EPC;
-        u32x4 v = u32x4{0u, 0u, 0u, 0u};
-        if (t0 + tb < T && h < H) v = *reinterpret_cast<const u32x4*>(x + (t0 + tb) * H + h);
-        *reinterpret_cast<u32x4*>(s_x + tb * W + h) = v;
+    for (int idx = threadIdx.x; idx < kTT * W / 8; idx += kTileWaves * 64) {
+        const int tb = idx / (W / 8), h = (idx % (W / 8)) * 8;
+        Chunk8<TIn> ch;
+        ch.zero();
+        if (t0 + tb < T && h < H) ch.load(x + (t0 + tb) * H + h);
+        float4 lo, hi;
+        lo.x = ch.get(0); lo.y = ch.get(1); lo.z = ch.get(2); lo.w = ch.get(3);
+        hi.x = ch.get(4); hi.y = ch.get(5); hi.z = ch.get(6); hi.w = ch.get(7);
+        *reinterpret_cast<float4*>(s_x + tb * W + h) = lo;
+        *reinterpret_cast<float4*>(s_x + tb * W + h + 4) = hi;
     }
     __syncthreads();
 
@@ -304,11 +310,9 @@ __global__ __launch_bounds__(kTileWaves * 64) void router_tile_kernel(
                 }
 #pragma unroll
                 for (int tt = 0; tt < kTT; ++tt) {
-                    Chunk8<TIn> xc;
-                    xc.load(s_x + tt * W + h0);
-                    float xv[8];
-#pragma unroll
-                    for (int i = 0; i < 8; ++i) xv[i] = xc.get(i);
+                    const float4 x0 = *reinterpret_cast<const float4*>(s_x + tt * W + h0);
+                    const float4 x1 = *reinterpret_cast<const float4*>(s_x + tt * W + h0 + 4);
+                    const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
 #pragma unroll
                     for (int ee = 0; ee < kEG; ++ee)
 #pragma unroll
