@@ -268,7 +268,6 @@ __global__ __launch_bounds__(kTileWaves * 64) void router_tile_kernel(
     int32_t* __restrict__ topk_ids) {
 #pragma clang fp contract(off)
     constexpr int W = NC * 512;
-    constexpr int EPC = 16 / sizeof(TIn);
     // x rows converted to fp32 once here, so the inner loop does no conversions for them
     __shared__ __attribute__((aligned(16))) float s_x[kTT * W];
     __shared__ float s_logits[kTT * 512];
