@@ -110,6 +110,9 @@ def main():
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-torch-baseline", action="store_true")
+    ap.add_argument("--e2e", action="store_true",
+                    help="instead: the end-to-end qwen3_moe driver (64 x 512-token prompts, "
+                         "256 greedy tokens, 48 random-init layers)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 1 GiB device copy (counter calibration for rocprofv3)")
@@ -125,6 +128,12 @@ def main():
         sys.exit(2)
 
     import torch
+    if args.e2e:
+        from tinyserve_amd.e2e import run_e2e
+        r = run_e2e()
+        print(json.dumps({"metric": "qwen3_moe end-to-end greedy generation (random-init "
+                                    "Qwen3-30B-A3B, bf16, one GPU)", "e2e": r}), flush=True)
+        return
     if args.copy_calibration:
         n = 1 << 30
         src = torch.empty(n, dtype=torch.uint8, device="cuda")
