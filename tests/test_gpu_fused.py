@@ -53,6 +53,9 @@ def test_fused_moe_full_size_token_subset(dev, tsm, qwen_layer):
     sel = torch.randperm(T, generator=torch.Generator().manual_seed(0))[:384]
     ref = moe_reference(x.cpu()[sel], w13c, w2c, w.cpu()[sel], ids.cpu().long()[sel])
     assert_close(out.cpu()[sel], ref, "T=8192 subset")
+    # the packed-weight prefill kernels (persistent 128-row tiles) give the same bits in full
+    p13, p2 = tsm.pack_moe_weights(w13, w2)
+    assert torch.equal(tsm.fused_moe_packed(x, p13, p2, w, ids), out)
 
 
 def test_rows_sum_topk_false(dev, tsm, qwen_layer):
