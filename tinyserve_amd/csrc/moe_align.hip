@@ -58,7 +58,10 @@ __global__ __launch_bounds__(kThreads) void align_place_kernel(
     __shared__ int base[kMaxBuckets];         // first output row of this slice's bucket-b run
     __shared__ int pend[kMaxBuckets];         // padded end of each bucket
     __shared__ int run[kMaxBuckets];          // placed so far in this slice
-    __shared__ int wcnt[kWaves][kMaxBuckets]; // per-wavefront counts of the current chunk
+    // per-wavefront counts of a chunk, double-buffered across chunks; after the prefix pass an
+    // entry holds the first row (within the bucket's run in this slice) of that wavefront's
+    // assignments of that bucket
+    __shared__ int wcnt[2][kWaves][kMaxBuckets];
     const int NB = E + 1;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int slice = blockIdx.x;
@@ -116,11 +119,13 @@ __global__ __launch_bounds__(kThreads) void align_place_kernel(
     int nbits = 1;
     while ((1 << nbits) <= NB) ++nbits;  // bucket values 0..NB (NB = out-of-range lane)
     const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    for (int i = tid; i < kWaves * NB; i += kThreads) wcnt[0][i / NB][i % NB] = 0;
+    __syncthreads();
     for (int c = 0; c < slice_chunks; ++c) {
         const int64_t chunk0 = s0 + (int64_t)c * kChunk;
         if (chunk0 >= numel) break;
-        for (int i = tid; i < kWaves * NB; i += kThreads) wcnt[i / NB][i % NB] = 0;
-        __syncthreads();
+        int (*cur)[kMaxBuckets] = wcnt[c & 1];
+        int (*nxt)[kMaxBuckets] = wcnt[(c + 1) & 1];
         const int64_t a = chunk0 + tid;
         const int b = a < numel ? bucket_of(ids[a], E) : NB;
         uint64_t same = ~0ull;
@@ -129,20 +134,23 @@ __global__ __launch_bounds__(kThreads) void align_place_kernel(
             same &= ((b >> bit) & 1) ? on : ~on;
         }
         const int rank = __popcll(same & lt_mask);
-        if (b < NB && rank == 0) wcnt[wave][b] = __popcll(same);
+        if (b < NB && rank == 0) cur[wave][b] = __popcll(same);
         __syncthreads();
-        if (b < NB) {
-            int pos = run[b] + rank;
-            for (int w = 0; w < wave; ++w) pos += wcnt[w][b];
-            sorted_ids[base[b] + pos] = (int32_t)a;
-        }
-        __syncthreads();
+        // per bucket: exclusive prefix over the wavefronts (stable: lower wavefronts first),
+        // starting at what earlier chunks placed; the other buffer is cleared for the next
+        // chunk (its readers, the previous chunk's placement, finished before the barrier)
         for (int bb = tid; bb < NB; bb += kThreads) {
-            int add = 0;
-            for (int w = 0; w < kWaves; ++w) add += wcnt[w][bb];
-            run[bb] += add;
+            int r = run[bb];
+            for (int w = 0; w < kWaves; ++w) {
+                const int n = cur[w][bb];
+                cur[w][bb] = r;
+                r += n;
+            }
+            run[bb] = r;
         }
+        for (int i = tid; i < kWaves * NB; i += kThreads) nxt[i / NB][i % NB] = 0;
         __syncthreads();
+        if (b < NB) sorted_ids[base[b] + cur[wave][b] + rank] = (int32_t)a;
     }
 
     // 4. padding rows and tile -> expert entries, one bucket per thread (rows [start+cnt, end)
