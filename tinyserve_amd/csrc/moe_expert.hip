@@ -24,8 +24,12 @@ namespace {
 
 constexpr int kMaxBucketsE = 513;
 
-template <int S, int NB, int WN, bool GATEUP, bool PACKED, bool SPEC>
+// MODE 0: workgroup column = expert index; 1: the same, with the weights requested before the
+// id scan (most experts have rows); 2 (compact, few assignments): workgroup column j takes the
+// j-th non-empty bucket of the ids, so the grid spans min(numel, experts) columns, not all E.
+template <int S, int NB, int WN, bool GATEUP, bool PACKED, int MODE>
 __global__ __launch_bounds__(256 * WN, 2) void moe_expert_kernel(ExpertArgs p) {
+    constexpr bool SPEC = MODE == 1, COMPACT = MODE == 2;
     static_assert(!GATEUP || NB == 2, "gate_up: one gate and one up block per wavefront group");
     constexpr int NT = 256 * WN;
     constexpr int OUTC = GATEUP ? 16 * WN : 16 * NB * WN;  // output columns per workgroup
@@ -34,11 +38,12 @@ __global__ __launch_bounds__(256 * WN, 2) void moe_expert_kernel(ExpertArgs p) {
     __shared__ int s_rows[kExpertMaxRows];
     __shared__ int s_wsum[NT / 64];
     __shared__ int s_start;
+    __shared__ int s_expert;
 
-    const int e = blockIdx.x / p.n_tiles, n_tile = blockIdx.x % p.n_tiles;
+    const int col = blockIdx.x / p.n_tiles, n_tile = blockIdx.x % p.n_tiles;
     const int tid = threadIdx.x, lane = tid & 63, wave = (tid >> 6) & 3, wgrp = tid >> 8;
     const int wid = tid >> 6;
-    const bool remote = (e == p.E);
+    int e = col;
 
     // 1. scan the ids: histogram (for e's start) and e's assignments in flat order. The ids
     // (at most kIdRegs per thread) are requested before the weights so their loads return first.
@@ -53,9 +58,9 @@ __global__ __launch_bounds__(256 * WN, 2) void moe_expert_kernel(ExpertArgs p) {
     // are expected to have rows (SPEC), after it otherwise (empty experts then cost no weights)
     const int r = lane & 15, q = lane >> 4;
     const int kbase = wave * (32 * S) + q * 8;  // this lane's first k; step s adds 32*s
-    const bf16_t* Be = p.B + (int64_t)e * (GATEUP ? 2 : 1) * p.N * p.K;
     u32x4 b[NB][S];
     auto load_b = [&]() {
+        const bf16_t* Be = p.B + (int64_t)e * (GATEUP ? 2 : 1) * p.N * p.K;
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
             const u32x4* src;
@@ -75,10 +80,44 @@ __global__ __launch_bounds__(256 * WN, 2) void moe_expert_kernel(ExpertArgs p) {
             for (int s = 0; s < S; ++s) b[nb][s] = __builtin_nontemporal_load(src + stride * s);
         }
     };
-    if (SPEC && !remote) load_b();
+    if (SPEC && e != p.E) load_b();
 
     for (int bk = tid; bk <= p.E; bk += NT) s_hist[bk] = 0;
     __syncthreads();
+    if (COMPACT) {
+        // histogram first, then this column's bucket: the col-th non-empty one in order
+        // (0..E-1 for gate_up; 0..E for down, E being the remote bucket)
+#pragma unroll
+        for (int c = 0; c < kIdRegs; ++c) {
+            if ((int64_t)c * NT >= p.numel) break;
+            const int64_t i = (int64_t)c * NT + tid;
+            if (i < p.numel) {
+                const int id = idr[c];
+                atomicAdd(&s_hist[(id >= 0 && id < p.E) ? id : p.E], 1);
+            }
+        }
+        __syncthreads();
+        if (wid == 0) {
+            const int nb_all = GATEUP ? p.E : p.E + 1;
+            int seen = 0, found = -1;
+            for (int base = 0; base < nb_all && found < 0; base += 64) {
+                const bool nz = base + lane < nb_all && s_hist[base + lane] > 0;
+                const uint64_t bal = __ballot(nz);
+                const int n = __popcll(bal);
+                if (col < seen + n) {
+                    const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+                    if (nz && seen + __popcll(bal & lt) == col) s_expert = base + lane;
+                    found = 1;
+                }
+                seen += n;
+            }
+            if (found < 0 && lane == 0) s_expert = -1;
+        }
+        __syncthreads();
+        e = s_expert;
+        if (e < 0) return;  // fewer non-empty buckets than columns
+    }
+    const bool remote = (e == p.E);
     int count = 0;
 #pragma unroll
     for (int c = 0; c < kIdRegs; ++c) {
@@ -86,7 +125,7 @@ __global__ __launch_bounds__(256 * WN, 2) void moe_expert_kernel(ExpertArgs p) {
         const int64_t i = (int64_t)c * NT + tid;
         const int id = idr[c];
         const bool in = i < p.numel;
-        if (in) atomicAdd(&s_hist[(id >= 0 && id < p.E) ? id : p.E], 1);
+        if (!COMPACT && in) atomicAdd(&s_hist[(id >= 0 && id < p.E) ? id : p.E], 1);
         const bool match = in && (remote ? (id < 0 || id >= p.E) : id == e);
         const uint64_t bal = __ballot(match);
         const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
@@ -181,13 +220,19 @@ __global__ __launch_bounds__(256 * WN, 2) void moe_expert_kernel(ExpertArgs p) {
 template <int S, int NB, bool GATEUP, bool PACKED, int WN = 1>
 void launch_e(const ExpertArgs& g, hipStream_t stream) {
     const int experts = g.E + (GATEUP ? 0 : 1);
-    // speculative weight loads once an expert is expected to see >= 2 assignments
-    if (g.numel >= 2ll * g.E)
-        hipLaunchKernelGGL((moe_expert_kernel<S, NB, WN, GATEUP, PACKED, true>),
+    if (2 * g.numel < g.E) {
+        // few assignments: one workgroup column per non-empty bucket (at most numel of them)
+        const int cols = (int)(g.numel < experts ? g.numel : experts);
+        hipLaunchKernelGGL((moe_expert_kernel<S, NB, WN, GATEUP, PACKED, 2>),
+                           dim3(cols * g.n_tiles), dim3(256 * WN), 0, stream, g);
+    } else if (g.numel >= 2ll * g.E) {
+        // speculative weight loads once an expert is expected to see >= 2 assignments
+        hipLaunchKernelGGL((moe_expert_kernel<S, NB, WN, GATEUP, PACKED, 1>),
                            dim3(experts * g.n_tiles), dim3(256 * WN), 0, stream, g);
-    else
-        hipLaunchKernelGGL((moe_expert_kernel<S, NB, WN, GATEUP, PACKED, false>),
+    } else {
+        hipLaunchKernelGGL((moe_expert_kernel<S, NB, WN, GATEUP, PACKED, 0>),
                            dim3(experts * g.n_tiles), dim3(256 * WN), 0, stream, g);
+    }
 }
 
 // gate_up with WN wavefront groups (16 activation columns each) per workgroup.

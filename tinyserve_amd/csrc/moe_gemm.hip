@@ -246,18 +246,17 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const bf16_t* __restrict_
 
 // ---- kernel table --------------------------------------------------------------------------
 // Tile height per batch size. block_m == 0: expert-major weight streaming (moe_expert.hip, no
-// permutation step) for E/2 <= numel <= 16E (from 2E on with the weights requested before the id
-// scan); below E/2 nearly every expert is empty and the 16-row streaming tiles over the permuted
-// rows launch far fewer workgroups. Otherwise reference-layout weights use 64-row LDS tiles (the
-// reference's BLOCK_M switch is at 4E, tinykernels.py:1779); packed weights use 64-row pipelined
-// tiles up to 32E and 128-row above.
+// permutation step) up to numel = 16E: from 2E on with the weights requested before the id scan,
+// below E/2 with one workgroup column per non-empty expert instead of per expert. Otherwise
+// reference-layout weights use 64-row LDS tiles (the reference's BLOCK_M switch is at 4E,
+// tinykernels.py:1779); packed weights use 64-row pipelined tiles up to 32E and 128-row above.
 struct Plan {
     int block_m;
 };
 
 Plan plan_for(int64_t T, int H, int I, int E, int top_k, bool packed) {
     const int64_t numel = T * top_k;
-    if (2 * numel >= E && numel <= 16ll * E && expert_path_supported(numel, H, I, E))
+    if (numel >= 1 && numel <= 16ll * E && expert_path_supported(numel, H, I, E))
         return Plan{0};
     if (numel <= 4ll * E) return Plan{16};
     if (!packed || numel <= 32ll * E) return Plan{64};
