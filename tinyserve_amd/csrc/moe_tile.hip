@@ -22,6 +22,8 @@
 // Reference computation: _fused_moe_kernel (tinykernels.py:1589-1765), epilogues as in the
 // weight-streaming kernels (SwiGLU with the reference's bf16 rounding points; routing-weight
 // scaling and scatter to assignment order).
+#include <type_traits>
+
 #include "common.h"
 #include "internal.h"
 #include "tinyserve_moe.h"
@@ -144,9 +146,13 @@ __global__ __launch_bounds__(64 * kNW, 1) void moe_tile_kernel(GemmArgs p) {
     const int chunk_end = chunk_begin + q8 + (xcd < r8 ? 1 : 0);
 
     // Load sources. A: wavefront w issues the 8-row groups w + 8j (element offsets of each lane's
-    // row and swizzled chunk). B: instruction index w + 8j is block (nb, kk) = ((w >> 1) + 4j,
+    // row and swizzled chunk; gate_up rows are gathered from all of x, so 64-bit, while down's
+    // rows are the tile's own consecutive rows, so a 32-bit offset from the tile's first row,
+    // a_base, which is uniform). B: instruction index w + 8j is block (nb, kk) = ((w >> 1) + 4j,
     // w & 1), so one base pointer plus j * b_jstride covers the wavefront's loads.
-    uint32_t a_src[LPA];
+    using a_off_t = typename std::conditional<GATEUP, uint64_t, uint32_t>::type;
+    a_off_t a_src[LPA];
+    const bf16_t* a_base = p.A;
     const bf16_t* b_src = nullptr;
     int64_t b_jstride = 0;
     int expert = -1, m0 = 0, n_tile = 0;
@@ -199,10 +205,11 @@ __global__ __launch_bounds__(64 * kNW, 1) void moe_tile_kernel(GemmArgs p) {
                 if (flat >= p.numel) flat = 0;  // padding row: any valid row, discarded
                 src_row = flat / p.top_k;
             } else {
-                src_row = m0 + (wave + j * kNW) * 8 + rr;
+                src_row = (wave + j * kNW) * 8 + rr;
             }
-            a_src[j] = (uint32_t)src_row * (uint32_t)p.K + c * 8;
+            a_src[j] = (a_off_t)src_row * (a_off_t)p.K + c * 8;
         }
+        if (!GATEUP) a_base = p.A + (int64_t)m0 * p.K;
         const bf16_t* Be = p.B + (int64_t)expert * (GATEUP ? 2 : 1) * p.N * p.K;
         b_src = Be + ((int64_t)(n_tile * NBK + (wave >> 1)) * KS + (wave & 1)) * 512 + lane * 8;
         b_jstride = (int64_t)4 * KS * 512;
@@ -211,7 +218,7 @@ __global__ __launch_bounds__(64 * kNW, 1) void moe_tile_kernel(GemmArgs p) {
         char* base = lds + (st & 1) * A_BYTES;
 #pragma unroll
         for (int j = 0; j < LPA; ++j)
-            __builtin_amdgcn_global_load_lds((const void*)(p.A + a_src[j] + st * 64),
+            __builtin_amdgcn_global_load_lds((const void*)(a_base + a_src[j] + st * 64),
                                              (lds_void*)(base + (wave + j * kNW) * kBlk), 16, 0,
                                              0);
     };
