@@ -228,6 +228,7 @@ def main():
             st.append(dict(
                 w=torch.empty(T, K_TOP, dtype=torch.float32, device=dev),
                 ids=torch.empty(T, K_TOP, dtype=torch.int32, device=dev),
+                logits=torch.empty(T, E, dtype=torch.float32, device=dev),
                 sorted_ids=torch.empty(mp, dtype=torch.int32, device=dev),
                 eids=torch.empty(mp // bm if bm else 1, dtype=torch.int32, device=dev),
                 total=torch.empty(1, dtype=torch.int32, device=dev),
@@ -241,7 +242,7 @@ def main():
         def router(i):
             c = st[i]
             check(lib.tsm_moe_router(ptr(xs[i]), ptr(layers[i][0]), 1, T, H, E, K_TOP, 1, None,
-                                     None, 0, None, ptr(c["w"]), ptr(c["ids"]), cur()), "router")
+                                     None, 0, ptr(c["logits"]), ptr(c["w"]), ptr(c["ids"]), cur()), "router")
 
         def align(i):
             c = st[i]

@@ -67,12 +67,14 @@ int tsm_moe_route(const void* logits, int logits_dtype, int64_t T, int E, int64_
 
 /*
  * Fused router: gate GEMM (fp32 accumulation with a fixed summation order) + optional per-expert
- * fp32 bias + optional rounding of the logits to bf16 + the routing of tsm_moe_route, one launch.
+ * fp32 bias + optional rounding of the logits to bf16 + the routing of tsm_moe_route. One launch;
+ * with logits_out given and T <= 256, two (the gate GEMM spread over expert slices into
+ * logits_out, then the selection from it), which is lower latency at decode sizes.
  * Replaces `self.gate(x)` followed by tk.moe_route in SparseMoE.forward (serve.py:1079-1080).
  * x: [T, H], gate_w: [E, H], both of dtype `dtype` (TSM_BF16 or TSM_F32). bias: [E] fp32 or null.
  * logits_bf16 != 0 rounds each logit to bf16 (round-to-nearest-even) before the softmax, as the
  * reference's bf16 nn.Linear output is. logits_out: [T, E] fp32 or null (the logits the softmax
- * saw). Requires H % 8 == 0, H <= 8192, and the tsm_moe_route limits.
+ * saw). Requires H % 8 == 0, 8 <= H <= 4096, and the tsm_moe_route limits.
  */
 int tsm_moe_router(const void* x, const void* gate_w, int dtype, int64_t T, int H, int E,
                    int top_k, int renorm, const int64_t* expert_map, const float* bias,

@@ -109,8 +109,8 @@ def test_router_matches_torch_closed_form(dev, tsm, qwen_layer):
 @pytest.mark.parametrize("T", [1, 64, 256])
 @pytest.mark.parametrize("logits_bf16", [False, True])
 def test_router_single_launch_without_logits_buffer(dev, tsm, qwen_layer, T, logits_bf16):
-    """tsm_moe_router without a logits buffer (as the fused forward calls it) gives the same bits
-    as with one."""
+    """tsm_moe_router without a logits buffer (one kernel per token) gives the same bits as with
+    one (the gate GEMM split over expert slices, then selection from the buffer)."""
     from tinyserve_amd import _lib
     print(f"router single-launch T={T} logits_bf16={logits_bf16}", flush=True)
     (gate_w, _, _), _ = qwen_layer

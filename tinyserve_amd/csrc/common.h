@@ -85,25 +85,30 @@ __device__ __forceinline__ float wave_max(float v) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
-// (largest value, lowest index among equal values) over the wavefront.
+// (largest value, lowest index among equal values) over the wavefront, for values that are
+// +0 or more, or -inf. In that domain the IEEE bit patterns order like signed integers, so the
+// pair is one order-preserving 64-bit key, (bits ^ sign) << 32 | ~index, and every step is a
+// 64-bit compare and two selects with no branches.
 template <int CTRL, int ROW_MASK>
-__device__ __forceinline__ void argmax_step(float& bv, int& bi) {
-    const float ov = __int_as_float(dpp_i<CTRL, ROW_MASK>(__float_as_int(bv)));
-    const int oi = dpp_i<CTRL, ROW_MASK>(bi);
-    const bool take = ov > bv || (ov == bv && oi < bi);
-    bv = take ? ov : bv;
-    bi = take ? oi : bi;
+__device__ __forceinline__ void key_max_step(uint32_t& hi, uint32_t& lo) {
+    const uint32_t ohi = (uint32_t)dpp_i<CTRL, ROW_MASK>((int)hi);
+    const uint32_t olo = (uint32_t)dpp_i<CTRL, ROW_MASK>((int)lo);
+    const uint64_t k = ((uint64_t)hi << 32) | lo, o = ((uint64_t)ohi << 32) | olo;
+    const bool take = o > k;
+    hi = take ? ohi : hi;
+    lo = take ? olo : lo;
 }
 
 __device__ __forceinline__ void wave_argmax(float& bv, int& bi) {
-    argmax_step<0xB1, 0xF>(bv, bi);
-    argmax_step<0x4E, 0xF>(bv, bi);
-    argmax_step<0x141, 0xF>(bv, bi);
-    argmax_step<0x140, 0xF>(bv, bi);
-    argmax_step<0x142, 0xA>(bv, bi);
-    argmax_step<0x143, 0xC>(bv, bi);
-    bv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bv), 63));
-    bi = __builtin_amdgcn_readlane(bi, 63);
+    uint32_t hi = __float_as_uint(bv) ^ 0x80000000u, lo = ~(uint32_t)bi;
+    key_max_step<0xB1, 0xF>(hi, lo);   // quad_perm [1,0,3,2]
+    key_max_step<0x4E, 0xF>(hi, lo);   // quad_perm [2,3,0,1]
+    key_max_step<0x141, 0xF>(hi, lo);  // row_half_mirror
+    key_max_step<0x140, 0xF>(hi, lo);  // row_mirror
+    key_max_step<0x142, 0xA>(hi, lo);  // row_bcast:15 into rows 1 and 3
+    key_max_step<0x143, 0xC>(hi, lo);  // row_bcast:31 into rows 2 and 3
+    bv = __uint_as_float(__builtin_amdgcn_readlane(hi, 63) ^ 0x80000000u);
+    bi = (int)~__builtin_amdgcn_readlane(lo, 63);
 }
 
 // exp(x) in fp32 for the router softmax, written out with explicit fmaf so the host oracle

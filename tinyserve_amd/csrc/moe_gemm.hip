@@ -266,7 +266,7 @@ Plan plan_for(int64_t T, int H, int I, int E, int top_k, bool packed) {
 constexpr int kBN = 128;  // B rows per workgroup tile (both variants)
 
 struct Layout {
-    size_t sorted, expert_ids, total, hist, act, rows, topk_w, topk_ids, bytes;
+    size_t sorted, expert_ids, total, hist, act, rows, topk_w, topk_ids, logits, bytes;
 };
 
 Layout layout_for(int64_t T, int H, int I, int E, int top_k, bool with_route) {
@@ -300,6 +300,7 @@ Layout layout_for(int64_t T, int H, int I, int E, int top_k, bool with_route) {
     if (with_route) {
         L.topk_w = take(sizeof(float) * numel);
         L.topk_ids = take(sizeof(int32_t) * numel);
+        L.logits = take(sizeof(float) * T * E);  // router logits, staged for the selection
     }
     L.bytes = off;
     return L;
@@ -549,7 +550,7 @@ static int moe_forward_impl(const void* x, const void* gate_w, const void* w13, 
     float* tw = topk_w ? topk_w : reinterpret_cast<float*>(w + L.topk_w);
     int32_t* ti = topk_ids ? topk_ids : reinterpret_cast<int32_t*>(w + L.topk_ids);
     rc = tsm_moe_router(x, gate_w, TSM_BF16, T, H, E, top_k, renorm, expert_map, bias,
-                        logits_bf16, nullptr, tw, ti, stream);
+                        logits_bf16, reinterpret_cast<float*>(w + L.logits), tw, ti, stream);
     if (rc) return rc;
     return run_experts(x, w13, w2, tw, ti, T, H, I, E, top_k, sum_topk, packed, out, w, L,
                        stream);

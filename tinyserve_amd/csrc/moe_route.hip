@@ -1,5 +1,6 @@
-// Router kernels: fp32 softmax + top-k + renormalisation, one wavefront per token, optionally
-// preceded by the router (gate) GEMM in the same launch.
+// Router kernels: fp32 softmax + top-k + renormalisation, optionally preceded by the router (gate)
+// GEMM in the same launch, or (decode sizes, logits buffer given) in a launch of its own spread
+// over expert slices.
 //
 // Reference behaviour: _moe_route_kernel / moe_route (tinykernels.py:1535-1583) and the torch router
 // branch of SparseMoE.forward (serve.py:1089-1096). Selection is on p = exp(l - max l) with the
@@ -20,14 +21,32 @@ namespace {
 
 constexpr int kMaxM = 8;          // experts per lane: E <= 512
 constexpr int kRouterWaves = 16;  // wavefronts per router workgroup
+// Largest batch routed by the split gate GEMM when a logits buffer is given
+constexpr int64_t kSplitMaxT = 256;
+
+// LDS words wave_select needs per wavefront: E <= 128 keys as (hi, lo) pairs, then up to 64
+// selected (p, index) pairs.
+constexpr int kSelectLds = 2 * 128 + 2 * 64;
+
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
 
 // Softmax numerators, top-k and weights for one token whose logits lane j holds at
-// v[q] = logit[j + 64 q]. Writes topk_w/topk_ids[0..k). All lanes of the wavefront must call it.
-// Top-k by repeated argmax over the wavefront (largest p, lowest expert index among equal p).
+// v[q] = logit[j + 64 q]. Writes topk_w/topk_ids[0..k). All lanes of the wavefront must call it;
+// `lds` is kSelectLds words of LDS owned by this wavefront.
+// Order: largest p first, the lowest expert index among equal p. Every p is +0 or more, so with
+// -inf for experts out of range its bits, sign-flipped, order like unsigned integers, and
+// key(e) = (bits(p_e) ^ sign) << 32 | ~e is a total order in which the selection is the k
+// largest keys. E <= 128: each key's rank (the number of larger keys) is counted directly,
+// and rank r < k is slot r; independent compares instead of k dependent rounds. Larger E:
+// k rounds of a wavefront argmax. Both give the same slots; sel_sum adds them in slot order.
 __device__ __forceinline__ void wave_select(float (&v)[kMaxM], int E, int top_k, int renorm,
                                             const int64_t* __restrict__ expert_map,
                                             float* __restrict__ out_w,
-                                            int32_t* __restrict__ out_ids) {
+                                            int32_t* __restrict__ out_ids, uint32_t* lds) {
 #pragma clang fp contract(off)
     const int lane = threadIdx.x & (kWave - 1);
     const int nq = (E + 63) >> 6;  // slots in use (uniform): the loops below skip the rest
@@ -50,23 +69,65 @@ __device__ __forceinline__ void wave_select(float (&v)[kMaxM], int E, int top_k,
 
     float sel_sum = 0.0f, my_v = 0.0f;
     int my_i = 0;
-    for (int s = 0; s < top_k; ++s) {
-        float bv = -__builtin_huge_valf();
-        int bi = 0x7fffffff;
+    if (nq <= 2) {
+        uint64_t* keys = reinterpret_cast<uint64_t*>(lds);
+        uint32_t* slots = lds + 2 * 128;
+        uint64_t mine[2];
 #pragma unroll
-        for (int q = 0; q < kMaxM; ++q)
-            if (q < nq) {
-                const bool take = v[q] > bv;  // ascending q: the lowest index wins ties
-                bv = take ? v[q] : bv;
-                bi = take ? lane + 64 * q : bi;
+        for (int q = 0; q < 2; ++q) {
+            const int e = lane + 64 * q;
+            mine[q] = e < E ? ((uint64_t)(__float_as_uint(v[q]) ^ 0x80000000u) << 32) |
+                                  (uint32_t)~e
+                            : 0;
+            if (q < nq) keys[e] = mine[q];
+        }
+        wave_lds_sync();
+        int rank[2][2] = {{0, 0}, {0, 0}};  // two accumulators per key
+#pragma unroll 4
+        for (int e2 = 0; e2 < 64 * nq; e2 += 2) {
+            const uint64_t k0 = keys[e2], k1 = keys[e2 + 1];
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                if (q < nq) {
+                    rank[q][0] += k0 > mine[q] ? 1 : 0;
+                    rank[q][1] += k1 > mine[q] ? 1 : 0;
+                }
             }
-        wave_argmax(bv, bi);
-        sel_sum = sel_sum + bv;
-        my_v = lane == s ? bv : my_v;
-        my_i = lane == s ? bi : my_i;
+        }
 #pragma unroll
-        for (int q = 0; q < kMaxM; ++q)
-            if (q < nq) v[q] = bi == lane + 64 * q ? -__builtin_huge_valf() : v[q];
+        for (int q = 0; q < 2; ++q) {
+            const int r = rank[q][0] + rank[q][1];
+            if (q < nq && lane + 64 * q < E && r < top_k) {
+                slots[2 * r] = __float_as_uint(v[q]);
+                slots[2 * r + 1] = (uint32_t)(lane + 64 * q);
+            }
+        }
+        wave_lds_sync();
+        for (int s = 0; s < top_k; ++s) sel_sum = sel_sum + __uint_as_float(slots[2 * s]);
+        if (lane < top_k) {
+            my_v = __uint_as_float(slots[2 * lane]);
+            my_i = (int)slots[2 * lane + 1];
+        }
+        wave_lds_sync();  // the caller may reuse the words
+    } else {
+        for (int s = 0; s < top_k; ++s) {
+            float bv = -__builtin_huge_valf();
+            int bi = 0x7fffffff;
+#pragma unroll
+            for (int q = 0; q < kMaxM; ++q)
+                if (q < nq) {
+                    const bool take = v[q] > bv;  // ascending q: the lowest index wins ties
+                    bv = take ? v[q] : bv;
+                    bi = take ? lane + 64 * q : bi;
+                }
+            wave_argmax(bv, bi);
+            sel_sum = sel_sum + bv;
+            my_v = lane == s ? bv : my_v;
+            my_i = lane == s ? bi : my_i;
+#pragma unroll
+            for (int q = 0; q < kMaxM; ++q)
+                if (q < nq) v[q] = bi == lane + 64 * q ? -__builtin_huge_valf() : v[q];
+        }
     }
     float denom = renorm ? sel_sum : wave_sum_butterfly(part);
     if (lane < top_k) {
@@ -90,6 +151,7 @@ __global__ __launch_bounds__(256) void route_logits_kernel(
     const TLog* __restrict__ logits, int64_t T, int E, int64_t ld, int top_k, int renorm,
     const int64_t* __restrict__ expert_map, float* __restrict__ topk_w,
     int32_t* __restrict__ topk_ids) {
+    __shared__ __attribute__((aligned(16))) uint32_t s_sel[4][kSelectLds];
     const int w = threadIdx.x >> 6;
     const int64_t t = (int64_t)blockIdx.x * 4 + w;
     if (t >= T) return;
@@ -100,7 +162,95 @@ __global__ __launch_bounds__(256) void route_logits_kernel(
         int e = lane + 64 * q;
         v[q] = e < E ? load_logit<TLog>(logits, t * ld + e) : 0.0f;
     }
-    wave_select(v, E, top_k, renorm, expert_map, topk_w + t * top_k, topk_ids + t * top_k);
+    wave_select(v, E, top_k, renorm, expert_map, topk_w + t * top_k, topk_ids + t * top_k,
+                s_sel[w]);
+}
+
+// E <= 128: one token per 256-thread workgroup. The same selection as wave_select's rank
+// path with the rank counts split over the four wavefronts (wavefront w compares against keys
+// [32w, 32w + 32)); the integer partial ranks are then summed, so the slots are the same.
+template <typename TLog>
+__global__ __launch_bounds__(256) void route_rank_kernel(
+    const TLog* __restrict__ logits, int E, int64_t ld, int top_k, int renorm,
+    const int64_t* __restrict__ expert_map, float* __restrict__ topk_w,
+    int32_t* __restrict__ topk_ids) {
+#pragma clang fp contract(off)
+    __shared__ uint64_t s_keys[128];
+    __shared__ int s_rank[4][128];
+    __shared__ uint32_t s_slots[2 * 64];
+    const int w = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int64_t t = blockIdx.x;
+    const int nq = (E + 63) >> 6;
+    float v[2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        const int e = lane + 64 * q;
+        v[q] = e < E ? load_logit<TLog>(logits, t * ld + e) : -__builtin_huge_valf();
+    }
+    float m = wave_max(fmaxf(v[0], v[1]));
+    float part = 0.0f;
+    uint64_t mine[2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        const int e = lane + 64 * q;
+        const bool in = e < E;
+        if (q < nq) {
+            const float pe = router_expf(v[q] - m);
+            v[q] = in ? pe : -__builtin_huge_valf();
+            part = in ? part + pe : part;
+        }
+        mine[q] = in ? ((uint64_t)(__float_as_uint(v[q]) ^ 0x80000000u) << 32) | (uint32_t)~e : 0;
+        if (w == 0 && q < nq) s_keys[e] = mine[q];
+    }
+    __syncthreads();
+    const int n = 64 * nq;
+    int r[2][2] = {{0, 0}, {0, 0}};
+#pragma unroll
+    for (int j = 0; j < 32; j += 2) {
+        const int e2 = w * (n / 4) + j;
+        if (j < n / 4) {
+            const uint64_t k0 = s_keys[e2], k1 = s_keys[e2 + 1];
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                r[q][0] += k0 > mine[q] ? 1 : 0;
+                r[q][1] += k1 > mine[q] ? 1 : 0;
+            }
+        }
+    }
+#pragma unroll
+    for (int q = 0; q < 2; ++q) s_rank[w][lane + 64 * q] = r[q][0] + r[q][1];
+    __syncthreads();
+    if (w != 0) return;
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        const int e = lane + 64 * q;
+        const int rk = s_rank[0][e] + s_rank[1][e] + s_rank[2][e] + s_rank[3][e];
+        if (q < nq && e < E && rk < top_k) {
+            s_slots[2 * rk] = __float_as_uint(v[q]);
+            s_slots[2 * rk + 1] = (uint32_t)e;
+        }
+    }
+    wave_lds_sync();
+    float sel_sum = 0.0f;
+    for (int s = 0; s < top_k; ++s) sel_sum = sel_sum + __uint_as_float(s_slots[2 * s]);
+    const float denom = renorm ? sel_sum : wave_sum_butterfly(part);
+    if (lane < top_k) {
+        const int my_i = (int)s_slots[2 * lane + 1];
+        topk_w[t * top_k + lane] = __uint_as_float(s_slots[2 * lane]) / denom;
+        topk_ids[t * top_k + lane] = expert_map ? (int32_t)expert_map[my_i] : (int32_t)my_i;
+    }
+}
+
+template <typename TLog>
+void launch_route_logits(const TLog* logits, int64_t T, int E, int64_t ld, int top_k, int renorm,
+                         const int64_t* expert_map, float* w, int32_t* ids, hipStream_t stream) {
+    if (E <= 128)
+        hipLaunchKernelGGL(route_rank_kernel<TLog>, dim3((unsigned)T), dim3(256), 0, stream,
+                           logits, E, ld, top_k, renorm, expert_map, w, ids);
+    else
+        hipLaunchKernelGGL(route_logits_kernel<TLog>, dim3((unsigned)((T + 3) / 4)), dim3(256),
+                           0, stream, logits, T, E, ld, top_k, renorm, expert_map, w, ids);
 }
 
 // Eight consecutive inputs (16 bytes of bf16 or 32 bytes of fp32), kept raw until used.
@@ -179,7 +329,7 @@ __global__ __launch_bounds__(kRouterWaves * 64) void router_kernel(
     int logits_bf16, float* __restrict__ logits_out, float* __restrict__ topk_w,
     int32_t* __restrict__ topk_ids) {
 #pragma clang fp contract(off)
-    __shared__ float s_logits[64 * kMaxM];
+    __shared__ __attribute__((aligned(16))) float s_logits[64 * kMaxM];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int64_t t = blockIdx.x;
@@ -245,7 +395,59 @@ __global__ __launch_bounds__(kRouterWaves * 64) void router_kernel(
             int ee = lane + 64 * q;
             v[q] = ee < E ? s_logits[ee] : 0.0f;
         }
-        wave_select(v, E, top_k, renorm, expert_map, topk_w + t * top_k, topk_ids + t * top_k);
+        wave_select(v, E, top_k, renorm, expert_map, topk_w + t * top_k, topk_ids + t * top_k,
+                    reinterpret_cast<uint32_t*>(s_logits));
+    }
+}
+
+// Decode-sized batches with a logits buffer: the gate GEMM spread over (token, expert slice)
+// workgroups, so the gate matrix is read by many CUs at once instead of by one CU per token.
+// Wavefront w of slice s owns experts (s * WAVES + w) * EPW + j, j < EPW; the per-lane fma
+// chains and the reduce-scatter are those of router_kernel, so every logit is bit-identical.
+// Selection then runs from the buffer.
+template <typename TIn, int NC, int EPW, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void router_split_kernel(
+    const TIn* __restrict__ x, const TIn* __restrict__ gw, int H, int E,
+    const float* __restrict__ bias, int logits_bf16, float* __restrict__ logits) {
+#pragma clang fp contract(off)
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int64_t t = blockIdx.x;
+    const int e0 = (blockIdx.y * WAVES + wave) * EPW;
+    if (e0 >= E) return;
+
+    Chunk8<TIn> xc[NC], gc[EPW][NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const int h0 = c * 512 + lane * 8;
+        xc[c].zero();
+        if (h0 < H) xc[c].load(x + t * H + h0);
+#pragma unroll
+        for (int j = 0; j < EPW; ++j) {
+            gc[j][c].zero();
+            if (e0 + j < E && h0 < H) gc[j][c].load(gw + (int64_t)(e0 + j) * H + h0);
+        }
+    }
+    float acc[EPW];
+#pragma unroll
+    for (int j = 0; j < EPW; ++j) {
+        float a = 0.0f;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            if (c * 512 + lane * 8 < H) {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) a = __builtin_fmaf(xc[c].get(i), gc[j][c].get(i), a);
+            }
+        }
+        acc[j] = a;
+    }
+    float l = wave_reduce_scatter<EPW>(acc);
+    constexpr int kShift = EPW == 1 ? 6 : EPW == 2 ? 5 : EPW == 4 ? 4 : 3;
+    const int e = e0 + (lane >> kShift);
+    if ((lane & ((1 << kShift) - 1)) == 0 && e < E) {
+        if (bias) l = l + bias[e];
+        if (logits_bf16) l = round_bf16(l);
+        logits[t * E + e] = l;
     }
 }
 
@@ -270,7 +472,7 @@ __global__ __launch_bounds__(kTileWaves * 64) void router_tile_kernel(
     constexpr int W = NC * 512;
     // x rows converted to fp32 once here, so the inner loop does no conversions for them
     __shared__ __attribute__((aligned(16))) float s_x[kTT * W];
-    __shared__ float s_logits[kTT * 512];
+    __shared__ __attribute__((aligned(16))) float s_logits[kTT * 512];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int64_t t0 = (int64_t)blockIdx.x * kTT;
@@ -341,7 +543,8 @@ __global__ __launch_bounds__(kTileWaves * 64) void router_tile_kernel(
             int e = lane + 64 * q;
             v[q] = e < E ? s_logits[tb * 512 + e] : 0.0f;
         }
-        wave_select(v, E, top_k, renorm, expert_map, topk_w + t * top_k, topk_ids + t * top_k);
+        wave_select(v, E, top_k, renorm, expert_map, topk_w + t * top_k, topk_ids + t * top_k,
+                    reinterpret_cast<uint32_t*>(s_logits + tb * 512));
     }
 }
 
@@ -368,6 +571,28 @@ hipError_t launch_router_decode(const void* x, const void* gw, int64_t T, int H,
     return hipGetLastError();
 }
 
+template <typename TIn, int NC>
+hipError_t launch_router_split(const void* x, const void* gw, int64_t T, int H, int E,
+                               int top_k, int renorm, const int64_t* expert_map,
+                               const float* bias, int logits_bf16, float* logits, float* w,
+                               int32_t* ids, hipStream_t stream) {
+    constexpr int kW = 4;
+    if (T <= 8) {
+        hipLaunchKernelGGL((router_split_kernel<TIn, NC, 1, kW>),
+                           dim3((unsigned)T, (unsigned)((E + kW - 1) / kW)), dim3(kW * 64), 0,
+                           stream, (const TIn*)x, (const TIn*)gw, H, E, bias, logits_bf16, logits);
+    } else {
+        // one token per workgroup: tiling tokens (each gate row serving several) measured no
+        // faster at decode sizes, where the launch is latency-bound rather than L2-bound
+        hipLaunchKernelGGL((router_split_kernel<TIn, NC, 2, kW>),
+                           dim3((unsigned)T, (unsigned)((E + 2 * kW - 1) / (2 * kW))),
+                           dim3(kW * 64), 0, stream, (const TIn*)x, (const TIn*)gw, H, E, bias,
+                           logits_bf16, logits);
+    }
+    launch_route_logits<float>(logits, T, E, E, top_k, renorm, expert_map, w, ids, stream);
+    return hipGetLastError();
+}
+
 // Decode-sized batches: one token per workgroup (more workgroups, lower latency), experts per
 // wavefront rounded up to a power of two. Larger batches: 8-token tiles.
 template <typename TIn, int NC>
@@ -378,6 +603,9 @@ hipError_t launch_router_nc(const void* x, const void* gw, int64_t T, int H, int
     if (T > 256)
         return launch_router_tile<TIn, NC>(x, gw, T, H, E, top_k, renorm, expert_map, bias,
                                            logits_bf16, logits_out, w, ids, stream);
+    if (logits_out && T <= kSplitMaxT)
+        return launch_router_split<TIn, NC>(x, gw, T, H, E, top_k, renorm, expert_map, bias,
+                                            logits_bf16, logits_out, w, ids, stream);
     const int epw = (E + kRouterWaves - 1) / kRouterWaves;
 #define TSM_DEC(N)                                                                             \
     if (epw <= N)                                                                              \
@@ -434,15 +662,12 @@ extern "C" int tsm_moe_route(const void* logits, int logits_dtype, int64_t T, in
     TSM_REQUIRE(ld >= E, TSM_E_ARG, "ld (%lld) must be >= E (%d)", (long long)ld, E);
     if (T == 0) return TSM_OK;
     TSM_REQUIRE(logits && topk_w && topk_ids, TSM_E_ARG, "null pointer argument");
-    const unsigned blocks = (unsigned)((T + 3) / 4);
     if (logits_dtype == TSM_F32) {
-        hipLaunchKernelGGL(route_logits_kernel<float>, dim3(blocks), dim3(256), 0, stream,
-                           (const float*)logits, T, E, ld, top_k, renorm, expert_map, topk_w,
-                           topk_ids);
+        launch_route_logits<float>((const float*)logits, T, E, ld, top_k, renorm, expert_map,
+                                   topk_w, topk_ids, stream);
     } else if (logits_dtype == TSM_BF16) {
-        hipLaunchKernelGGL(route_logits_kernel<bf16_t>, dim3(blocks), dim3(256), 0, stream,
-                           (const bf16_t*)logits, T, E, ld, top_k, renorm, expert_map, topk_w,
-                           topk_ids);
+        launch_route_logits<bf16_t>((const bf16_t*)logits, T, E, ld, top_k, renorm, expert_map,
+                                    topk_w, topk_ids, stream);
     } else {
         set_error("logits dtype code %d not supported", logits_dtype);
         return TSM_E_DTYPE;
