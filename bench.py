@@ -119,6 +119,8 @@ def main():
     ap.add_argument("--traffic-json", default=os.path.join(
         os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic_gate_up_T64.json"),
                     help="HBM traffic per gate_up launch measured with rocprofv3 --pmc")
+    ap.add_argument("--block-m", type=int, default=None,
+                    help="stage timing with this tile height (0 = expert-major) instead of the plan's")
     ap.add_argument("--profile", action="store_true",
                     help="eager stage launches only (for rocprofv3 runs); no sweep, no CPU leg")
     args = ap.parse_args()
@@ -221,6 +223,8 @@ def main():
         xs = inputs(T, 1000 + T)
         numel = T * K_TOP
         bm = int(lib.tsm_moe_block_m(T, H, I, E, K_TOP, 1))  # 0: expert-major, no permutation
+        if args.block_m is not None:
+            bm = args.block_m
         mp = int(lib.tsm_moe_max_padded(numel, E, bm)) if bm else numel
         nws = int(lib.tsm_moe_align_workspace_size(numel, E, bm)) if bm else 0
         st = []

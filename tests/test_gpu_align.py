@@ -31,7 +31,8 @@ def gen_ids(kind, T, k, E, seed):
 
 CASES = [(1, 8, 128, 16), (8, 8, 128, 16), (64, 8, 128, 16), (256, 8, 128, 64),
          (1000, 8, 128, 64), (1024, 8, 128, 64), (1025, 8, 128, 64), (2048, 8, 128, 64),
-         (8192, 8, 128, 64), (64, 2, 8, 16), (3, 2, 3, 4), (4097, 3, 512, 128)]
+         (8192, 8, 128, 64), (64, 2, 8, 16), (3, 2, 3, 4), (4097, 3, 512, 128),
+         (100, 4, 16, 512), (2000, 8, 64, 256)]
 
 
 @pytest.mark.parametrize("T,k,E,bm", CASES)

@@ -246,8 +246,11 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const bf16_t* __restrict_
 
 // ---- kernel table --------------------------------------------------------------------------
 // Tile height per batch size. block_m == 0: expert-major weight streaming (moe_expert.hip, no
-// permutation step) up to numel = 16E: from 2E on with the weights requested before the id scan,
-// below E/2 with one workgroup column per non-empty expert instead of per expert. Otherwise
+// permutation step) up to numel = 12E (above that the align step plus 64-row pipelined tiles
+// measured faster with packed weights: T=256 of the Qwen3-30B layer 233 vs 256 us for the GEMM
+// stages; both layouts switch at the same size, so they keep giving the same bits): from 2E on
+// with the weights requested before the id scan, below E/2 with one workgroup column per
+// non-empty expert instead of per expert. Otherwise
 // reference-layout weights use 64-row LDS tiles (the reference's BLOCK_M switch is at 4E,
 // tinykernels.py:1779); packed weights use 64-row pipelined tiles up to 32E and 128-row above.
 struct Plan {
@@ -256,7 +259,7 @@ struct Plan {
 
 Plan plan_for(int64_t T, int H, int I, int E, int top_k, bool packed) {
     const int64_t numel = T * top_k;
-    if (numel >= 1 && numel <= 16ll * E && expert_path_supported(numel, H, I, E))
+    if (numel >= 1 && numel <= 12ll * E && expert_path_supported(numel, H, I, E))
         return Plan{0};
     if (numel <= 4ll * E) return Plan{16};
     if (!packed || numel <= 32ll * E) return Plan{64};
