@@ -1,0 +1,68 @@
+"""The stage entry points (align, gate_up, down, combine) at the pipelined tile heights.
+
+The 64- and 128-row tile kernels accumulate each output over K in one fp32 chain in the same
+order, so their outputs are equal bit for bit; the result also equals the planned
+fused_moe_packed at the same batch (a tile-kernel size) and, at a small batch, the oracle within
+the bf16 tolerance."""
+import pytest
+import torch
+
+from oracle.moe_oracle import make_layer, moe_reference
+
+pytestmark = pytest.mark.gpu
+
+
+def staged(tsm, x, p13, p2, w, ids, E, I, bm):
+    from tinyserve_amd import _lib
+    L = _lib.lib
+    T, H = x.shape
+    k = ids.shape[1]
+    numel = T * k
+    dev = x.device
+    mp = int(L.tsm_moe_max_padded(numel, E, bm))
+    nws = int(L.tsm_moe_align_workspace_size(numel, E, bm))
+    sorted_ids = torch.empty(mp, dtype=torch.int32, device=dev)
+    eids = torch.empty(mp // bm, dtype=torch.int32, device=dev)
+    total = torch.empty(1, dtype=torch.int32, device=dev)
+    aws = torch.empty(max(nws, 1), dtype=torch.uint8, device=dev)
+    act = torch.empty(mp, I, dtype=torch.bfloat16, device=dev)
+    rows = torch.empty(numel, H, dtype=torch.bfloat16, device=dev)
+    out = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
+    s = _lib.stream_of(x)
+    P = _lib.ptr
+    _lib.check(L.tsm_moe_align(P(ids), numel, E, bm, P(sorted_ids), P(eids), P(total), P(aws),
+                               nws, s), "align")
+    _lib.check(L.tsm_moe_gemm_gate_up(P(x), P(p13), P(sorted_ids), P(eids), P(total), numel, k,
+                                      H, I, E, bm, 1, P(act), s), f"gate_up bm={bm}")
+    _lib.check(L.tsm_moe_gemm_down(P(act), P(p2), P(w), P(sorted_ids), P(eids), P(total), numel,
+                                   H, I, E, bm, 1, P(rows), s), f"down bm={bm}")
+    _lib.check(L.tsm_moe_combine(P(rows), T, H, k, P(out), s), "combine")
+    torch.cuda.synchronize()
+    return out
+
+
+@pytest.mark.parametrize("H,I,E,k,T", [(2048, 768, 128, 8, 2048), (1024, 2816, 16, 2, 1500),
+                                       (768, 384, 32, 4, 700)])
+def test_tile_heights_agree(dev, tsm, H, I, E, k, T):
+    print(f"tile heights H={H} I={I} E={E} k={k} T={T}", flush=True)
+    x, gw, w13, w2 = make_layer(T, H, E, I, torch.bfloat16, seed=T + E, device=dev)
+    p13, p2 = tsm.pack_moe_weights(w13, w2)
+    w, ids, _ = tsm.moe_router(x, gw, k, True)
+    outs = {bm: staged(tsm, x, p13, p2, w, ids, E, I, bm) for bm in (64, 128)}
+    assert torch.equal(outs[64], outs[128]), "64 vs 128"
+    fused = tsm.fused_moe_packed(x, p13, p2, w, ids)
+    assert torch.equal(fused, outs[128])
+
+
+@pytest.mark.parametrize("bm", [64, 128])
+def test_tile_heights_against_oracle(dev, tsm, bm):
+    H, I, E, k, T = 768, 384, 32, 4, 40
+    x, gw, w13, w2 = make_layer(T, H, E, I, torch.bfloat16, seed=5, device=dev)
+    p13, p2 = tsm.pack_moe_weights(w13, w2)
+    w, ids, _ = tsm.moe_router(x, gw, k, True)
+    out = staged(tsm, x, p13, p2, w, ids, E, I, bm).float().cpu()
+    ref = moe_reference(x.cpu(), w13.cpu(), w2.cpu(), w.cpu(), ids.cpu().long()).float()
+    max_abs = (out - ref).abs().max().item()
+    mean_rel = ((out - ref).abs().mean() / ref.abs().mean()).item()
+    print(f"bm={bm} vs oracle: max_abs={max_abs:.3e} mean_rel={mean_rel:.3e}", flush=True)
+    assert max_abs <= 2e-2 and mean_rel <= 5e-3
