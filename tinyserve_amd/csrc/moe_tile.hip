@@ -22,6 +22,8 @@
 // Reference computation: _fused_moe_kernel (tinykernels.py:1589-1765), epilogues as in the
 // weight-streaming kernels (SwiGLU with the reference's bf16 rounding points; routing-weight
 // scaling and scatter to assignment order).
+#include <atomic>
+#include <mutex>
 #include <type_traits>
 
 #include "common.h"
@@ -491,18 +493,36 @@ __global__ __launch_bounds__(64 * kNW, 1) void moe_tile_kernel(GemmArgs p) {
     wait_vmcnt<0>();
 }
 
+// Per-device launch state: the CU count, and whether a kernel's dynamic-LDS limit has been raised
+// on that device (done once, under a lock, before the first launch there).
+constexpr int kMaxDevices = 64;
+
+int current_device() {
+    int dev = 0;
+    return hipGetDevice(&dev) == hipSuccess ? dev : 0;
+}
+
 int cu_count() {
-    static int cus = 0;
-    if (cus == 0) {
-        int dev = 0, n = 0;
-        if (hipGetDevice(&dev) == hipSuccess &&
-            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
-            n > 0)
-            cus = n;
-        else
-            cus = 256;
-    }
-    return cus;
+    static std::atomic<int> cus[kMaxDevices];
+    const int dev = current_device();
+    int n = dev < kMaxDevices ? cus[dev].load(std::memory_order_relaxed) : 0;
+    if (n > 0) return n;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+        n = 256;
+    if (dev < kMaxDevices) cus[dev].store(n, std::memory_order_relaxed);
+    return n;
+}
+
+// done[] belongs to one kernel (each launch_tile instantiation passes its own).
+void raise_lds_limit(const void* kernel, size_t lds, std::atomic<bool> (&done)[kMaxDevices]) {
+    static std::mutex mu;
+    const int dev = current_device();
+    if (dev < kMaxDevices && done[dev].load(std::memory_order_acquire)) return;
+    std::lock_guard<std::mutex> lock(mu);
+    if (dev < kMaxDevices && done[dev].load(std::memory_order_relaxed)) return;
+    (void)hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (dev < kMaxDevices) done[dev].store(true, std::memory_order_release);
 }
 
 template <int BM, bool GATEUP>
@@ -512,12 +532,8 @@ void launch_tile(GemmArgs g, hipStream_t stream) {
     constexpr int NB = (160 * 1024 - 2 * a_bytes) / b_bytes > 4 ? 4
                                                                  : (160 * 1024 - 2 * a_bytes) / b_bytes;
     const size_t lds = (size_t)2 * a_bytes + (size_t)NB * b_bytes;
-    static bool configured = false;
-    if (!configured) {
-        (void)hipFuncSetAttribute((const void*)moe_tile_kernel<BM, GATEUP, WM, NB>,
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        configured = true;
-    }
+    static std::atomic<bool> lds_raised[kMaxDevices];
+    raise_lds_limit((const void*)moe_tile_kernel<BM, GATEUP, WM, NB>, lds, lds_raised);
     // persistent: at most one workgroup per CU, a multiple of 8 so every XCD gets the same count
     const int64_t tiles = (int64_t)g.m_tiles * g.n_tiles;
     int64_t grid = tiles < cu_count() ? tiles : cu_count();
