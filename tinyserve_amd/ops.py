@@ -64,7 +64,8 @@ def _(logits, top_k, renormalize, expert_map=None):
 def moe_router(x: Tensor, gate_w: Tensor, top_k: int, renormalize: bool,
                expert_map: Optional[Tensor] = None, bias: Optional[Tensor] = None,
                logits_bf16: bool = False) -> Tuple[Tensor, Tensor, Tensor]:
-    """Gate GEMM + routing in one launch: -> (topk_weights, topk_ids, fp32 logits [T, E])."""
+    """Gate GEMM + routing: -> (topk_weights, topk_ids, fp32 logits [T, E]). One launch; two at
+    decode sizes (T <= 256: the gate GEMM spread over expert slices, then the selection)."""
     _on_gpu(x, gate_w, expert_map, bias)
     if x.dtype != gate_w.dtype or x.dtype not in (torch.bfloat16, torch.float32):
         raise TypeError(f"router needs x and gate weight both bf16 or both fp32, got "
