@@ -5,7 +5,8 @@ A step is one MoE layer forward (fused router + align + gate_up/SwiGLU + down + 
 batch of T synthetic tokens, inputs and weights resident in HBM. The headline workload is the
 decode configuration T=64 (H=2048, E=128, top-8, I=768); the step cycles over 8 distinct
 random-init layer copies so expert weights are streamed from HBM, not served from the 256 MB
-Infinity Cache. The timed region replays HIP graphs of the step (one graph per layer copy).
+Infinity Cache. The timed region replays a HIP graph of the 8 layer copies back to back (a
+model's decode graph runs its MoE layers the same way), timing exactly `--steps` layer steps.
 
 Prints ONE JSON line on stdout. Extra fields: per-stage kernel times (HIP events around each stage
 launch on the launch stream), the dominant kernel's roofline, a sweep over the decode/prefill
@@ -181,14 +182,15 @@ def main():
         return tsm.moe_forward(x, *layers[i], K_TOP, True, None, bias)
 
     def time_layer(T, steps, warmup, bias=None, use_packed=True):
-        """HIP-graph replays of the whole layer, cycling the layer copies. Returns (ms/step,
-        mean touched experts)."""
+        """HIP-graph replays of the whole layer, cycling the layer copies: one graph holds the L
+        copies back to back (as a model's decode graph runs its MoE layers), another the first
+        steps % L of them, so the timed region runs exactly `steps` layer steps, each on its own
+        weights, without a host graph launch per step. Returns (ms/step, mean touched experts)."""
         xs = inputs(T, 1000 + T)
         touched = []
         for i in range(L):
             _, ids, _ = tsm.moe_router(xs[i], layers[i][0], K_TOP, True, None, bias)
             touched.append(int(torch.unique(ids).numel()))
-        graphs = []
         s = torch.cuda.Stream()
         s.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(s):
@@ -196,22 +198,29 @@ def main():
                 forward(i, xs[i], bias, use_packed)
         torch.cuda.current_stream().wait_stream(s)
         torch.cuda.synchronize()
-        for i in range(L):
+
+        def capture(n):
             gr = torch.cuda.CUDAGraph()
             with torch.cuda.graph(gr):
-                forward(i, xs[i], bias, use_packed)
-            graphs.append(gr)
-        for j in range(warmup):
-            graphs[j % L].replay()
+                for i in range(n):
+                    forward(i, xs[i], bias, use_packed)
+            return gr
+        full = capture(L)
+        rem = steps % L
+        part = capture(rem) if rem else None
+        for _ in range(max(1, (warmup + L - 1) // L)):  # at least `warmup` untimed steps
+            full.replay()
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
-        for j in range(steps):
-            graphs[j % L].replay()
+        for _ in range(steps // L):
+            full.replay()
+        if part is not None:
+            part.replay()
         e1.record()
         torch.cuda.synchronize()
         ms = e0.elapsed_time(e1) / steps
-        del graphs
+        del full, part
         return ms, sum(touched) / len(touched)
 
     def time_stages(T, steps, warmup):
