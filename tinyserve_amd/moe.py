@@ -6,11 +6,13 @@ DecoderLayer that calls `self.mlp(h)` are unchanged:
     w13         [E_local, 2I, H]                   gate_proj rows, then up_proj rows
     w2          [E_local, H, I]                    down_proj
     expert_map  int64 [E]                          global id -> local id, -1 = another GPU's
-`forward` runs the fused router (gate GEMM + fp32 softmax/top-k/renormalise, one launch) and the
-experts (align, gate_up+SwiGLU, down, k-sum). With `router="linear"` it instead computes the
+`forward` runs the fused router (gate GEMM + fp32 softmax/top-k/renormalise) and the experts
+(align, gate_up+SwiGLU, down, k-sum). With `router="linear"` it instead computes the
 logits with self.gate (bf16, as the reference does) and routes them with moe_route.
 With `packed=True` (default) the experts run on an MFMA-tiled copy of w13/w2 (pack_moe_weights),
 made on the first forward after the parameters change (call `pack()` before HIP-graph capture).
+Changes are detected through the parameters' version counters, which in-place writes to the
+parameters or their views bump; after writing through `.data`, call `pack(force=True)`.
 Tensor parallelism is not part of this build: the result is this GPU's share (what the reference
 passes to tp_all_reduce).
 """
@@ -43,10 +45,10 @@ class SparseMoE(nn.Module):
         self._w13_packed = None
         self._w2_packed = None
 
-    def pack(self):
+    def pack(self, force: bool = False):
         """(Re)build the MFMA-tiled weight copies if w13/w2 changed since the last pack."""
         key = (self.w13.data_ptr(), self.w2.data_ptr(), self.w13._version, self.w2._version)
-        if key != self._packed_key:
+        if force or key != self._packed_key:
             with torch.no_grad():
                 self._w13_packed, self._w2_packed = ops.pack_moe_weights(self.w13, self.w2)
             self._packed_key = key
