@@ -106,7 +106,7 @@ __global__ __launch_bounds__(256 * WN, 2) void moe_expert_kernel(ExpertArgs p) {
                 const int n = __popcll(bal);
                 if (col < seen + n) {
                     const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-                    if (nz && seen + __popcll(bal & lt) == col) s_expert = base + lane;
+                    if (nz && seen + (int)__popcll(bal & lt) == col) s_expert = base + lane;
                     found = 1;
                 }
                 seen += n;

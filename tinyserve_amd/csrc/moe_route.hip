@@ -324,7 +324,7 @@ __device__ __forceinline__ float wave_reduce_scatter(float (&acc)[N]) {
 // wavefront 0 then selects from the logits in LDS.
 template <typename TIn, int NC, int EPW>
 __global__ __launch_bounds__(kRouterWaves * 64) void router_kernel(
-    const TIn* __restrict__ x, const TIn* __restrict__ gw, int64_t T, int H, int E, int top_k,
+    const TIn* __restrict__ x, const TIn* __restrict__ gw, int H, int E, int top_k,
     int renorm, const int64_t* __restrict__ expert_map, const float* __restrict__ bias,
     int logits_bf16, float* __restrict__ logits_out, float* __restrict__ topk_w,
     int32_t* __restrict__ topk_ids) {
@@ -566,7 +566,7 @@ hipError_t launch_router_decode(const void* x, const void* gw, int64_t T, int H,
                                 int logits_bf16, float* logits_out, float* w, int32_t* ids,
                                 hipStream_t stream) {
     hipLaunchKernelGGL((router_kernel<TIn, NC, EPW>), dim3((unsigned)T), dim3(kRouterWaves * 64),
-                       0, stream, (const TIn*)x, (const TIn*)gw, T, H, E, top_k, renorm,
+                       0, stream, (const TIn*)x, (const TIn*)gw, H, E, top_k, renorm,
                        expert_map, bias, logits_bf16, logits_out, w, ids);
     return hipGetLastError();
 }
