@@ -107,7 +107,8 @@ int tsm_silu_and_mul(const void* gate, int64_t gate_stride, const void* up, int6
  * Tile height (rows per expert tile) fused_moe uses for a batch of T tokens with the given weight
  * layout (TSM_LAYOUT_*). The reference picks 16 when T*k <= 4E, else 64 (tinykernels.py:1779);
  * this build picks from its own kernel table: 0 = the expert-major stages below (no tiles, no
- * permutation), else 16 / 64, and 128 for packed weights.
+ * permutation; T*k <= 12E within their size limits), else 16 (T*k <= 4E) / 64, and 128 for
+ * packed weights above 32E.
  */
 int tsm_moe_block_m(int64_t T, int H, int I, int E, int top_k, int weight_layout);
 
@@ -117,7 +118,7 @@ int tsm_moe_block_m(int64_t T, int H, int I, int E, int top_k, int weight_layout
  * Replaces fused_moe (tinykernels.py:1767-1796) with _moe_gemm/_fused_moe_kernel
  * (tinykernels.py:1589-1765) and silu_and_mul.
  * out: [T, H] bf16 when sum_topk != 0, else [T*k, H] bf16 (row t*k+s = weighted expert output of
- * slot s, zeros for remote slots). Requires H % 64 == 0, I % 64 == 0.
+ * slot s, zeros for remote slots). Requires H % 128 == 0, I % 64 == 0 (both >= 64).
  */
 size_t tsm_fused_moe_workspace_size(int64_t T, int H, int I, int E, int top_k);
 int tsm_fused_moe(const void* x, const void* w13, const void* w2, const float* topk_w,
