@@ -425,7 +425,13 @@ def main():
 
     if not args.no_cpu_baseline:
         from oracle.moe_oracle import moe_reference, route_torch
-        threads = torch.get_num_threads()
+        # Every core this process may run on, capped by the host-thread share the job is given
+        # (OMP_NUM_THREADS, when the launcher sets one): the torch-CPU path is then timed on all
+        # the cores it is allowed, and `cores` says how many that was.
+        affinity = len(os.sched_getaffinity(0))
+        share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+        threads = min(affinity, share) if share > 0 else affinity
+        torch.set_num_threads(threads)
         gw, w13, w2 = (t_.cpu() for t_ in layers[0])
         x = inputs(T, 1000 + T)[0].cpu()
         reps, t0 = 0, time.perf_counter()
@@ -440,7 +446,8 @@ def main():
         tc = el / reps
         nt_c = int(torch.unique(idc).numel())
         res["cpu_baseline"] = {"value": layer_bytes(T, nt_c) / tc / 1e9, "unit": "GB/s",
-                               "cores": threads, "kind": "port",
+                               "cores": threads, "host_cpus": os.cpu_count(),
+                               "affinity_cpus": affinity, "kind": "port",
                                "sample": f"{reps} layer forwards at T={T} (torch-CPU bf16 "
                                          f"restatement of serve.py router + moe_reference), "
                                          f"{el:.1f} s total, {tc * 1e3:.1f} ms/layer"}

@@ -189,6 +189,22 @@ int tsm_moe_forward(const void* x, const void* gate_w, const void* w13, const vo
  */
 int tsm_moe_pack_weights(const void* w, int64_t E, int N, int K, int interleave_halves, void* out,
                          hipStream_t stream);
+/*
+ * Packing with zero padding, for shapes the tile kernels do not take as they are (the reference's
+ * _fused_moe_kernel masks a ragged last K/N block instead, tinykernels.py:1719-1731; e.g. the
+ * one-GPU share of TP-8 for Qwen3-30B-A3B has I = 768/8 = 96). The source is [E, N, K]
+ * (interleave_halves: N = 2I, gate rows then up rows); the output is [E, N_pad, K_pad] in the
+ * packed layout above, with W read as zero outside the source. A padded row or column adds exact
+ * zeros to every product and sum, so outputs equal those of the unpadded problem.
+ * tsm_moe_padded_shape gives the sizes the *_packed entry points run at: H_pad = H and
+ * I_pad = I when the kernels take them, else H rounded up to a multiple of 128 and I to a
+ * multiple of 128. Pack w13 with (N, K, N_pad, K_pad) = (2I, H, 2 I_pad, H_pad) and w2 with
+ * (H, I, H_pad, I_pad); the *_packed entry points are then called with H = H_pad and I = I_pad,
+ * and x / out carry H_pad columns (x zero-padded; the extra output columns are zero).
+ */
+int tsm_moe_padded_shape(int H, int I, int* H_pad, int* I_pad);
+int tsm_moe_pack_weights_padded(const void* w, int64_t E, int N, int K, int N_pad, int K_pad,
+                                int interleave_halves, void* out, hipStream_t stream);
 int tsm_fused_moe_packed(const void* x, const void* w13p, const void* w2p, const float* topk_w,
                          const int32_t* topk_ids, int64_t T, int H, int I, int E, int top_k,
                          int sum_topk, void* out, void* ws, size_t ws_bytes, hipStream_t stream);

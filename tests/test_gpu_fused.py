@@ -109,6 +109,14 @@ def test_load_imbalance(dev, tsm, qwen_layer, kind):
     out = tsm.fused_moe(x, w13, w2, w, ids)
     ref = moe_reference(x.cpu(), w13c, w2c, w.cpu(), ids.cpu().long())
     assert_close(out, ref, kind)
+    # the default product path (packed weights: persistent 128-row tiles at this size, hot
+    # experts spanning many tiles) gives the same bits, and so matches the oracle too
+    p13, p2 = tsm.pack_moe_weights(w13, w2)
+    packed = tsm.fused_moe_packed(x, p13, p2, w, ids)
+    assert torch.equal(packed, out), kind
+    assert_close(packed, ref, f"{kind} packed")
+    whole = tsm.moe_forward_packed(x, gw, p13, p2, 8, True, None, bias.to(dev))
+    assert torch.equal(whole, out), kind
 
 
 @pytest.mark.parametrize("T", [1, 37, 64])
@@ -164,11 +172,17 @@ def test_sparse_moe_module(dev, tsm, qwen_layer):
             m.w2.copy_(w2)
             out = m(x)
             if router == "fused":
-                w, ids, _ = tsm.moe_router(x, gw, 8, True)
+                # a bf16 module rounds its logits to bf16, as the reference's bf16 Linear does
+                w, ids, _ = tsm.moe_router(x, gw, 8, True, None, None, True)
             else:
                 w, ids = tsm.moe_route(m.gate(x), 8, True, m.expert_map)
         ref = moe_reference(x.cpu(), w13c, w2c, w.cpu(), ids.cpu().long())
         assert_close(out, ref, f"SparseMoE {router} packed={packed}")
+        # the module holds one copy of its expert weights and hands back the reference layout
+        if packed:
+            assert m.weights_packed
+            sd = m.state_dict()
+            assert torch.equal(sd["w13"], w13) and torch.equal(sd["w2"], w2)
 
 
 def test_moe_forward_bf16_logits_mode(dev, tsm, qwen_layer):
@@ -283,3 +297,112 @@ def test_packed_expert_parallel_and_tiny(dev, tsm, qwen_layer):
     assert torch.equal(out, tsm.fused_moe(x, w13, w2, w, ids))
     ref = moe_reference(x.cpu(), w13.cpu(), w2.cpu(), w.cpu(), ids.cpu().long())
     assert_close(out, ref, "packed tiny T=2048")
+
+
+@pytest.mark.parametrize("T", [512, 2048])
+def test_packed_prefill_against_oracle(dev, tsm, qwen_layer, T):
+    """Prefill sizes on the default (packed) path against the oracle directly: T=512 runs the
+    64-row tile kernels, T=2048 the 128-row persistent tiles (a token subset is checked there;
+    each token's output depends only on its own row)."""
+    (gw, w13, w2), (_, w13c, w2c) = qwen_layer
+    p13, p2 = tsm.pack_moe_weights(w13, w2)
+    x = xrand(T, 2048, dev, 300 + T)
+    w, ids, _ = tsm.moe_router(x, gw, 8, True)
+    out = tsm.moe_forward_packed(x, gw, p13, p2, 8, True)
+    sel = torch.arange(T) if T <= 512 else \
+        torch.randperm(T, generator=torch.Generator().manual_seed(T))[:512]
+    ref = moe_reference(x.cpu()[sel], w13c, w2c, w.cpu()[sel], ids.cpu().long()[sel])
+    assert_close(out.cpu()[sel], ref, f"packed prefill T={T}")
+
+
+def test_pack_padded_matches_layout_definition(dev, tsm):
+    """The HIP packing kernel, with and without zero padding, against the tensor-permutation
+    statement of the layout (tinyserve_amd.layout, pinned on the CPU by test_layout), and the
+    inverse permutation restores the weights."""
+    from tinyserve_amd import layout
+    for E, I, H in ((3, 64, 256), (2, 96, 256), (2, 24, 200), (1, 50, 136)):
+        g = torch.Generator(device=dev).manual_seed(E * I + H)
+        w13 = torch.randn(E, 2 * I, H, generator=g, device=dev).bfloat16()
+        w2 = torch.randn(E, H, I, generator=g, device=dev).bfloat16()
+        Hp, Ip = tsm.ops.padded_shape(H, I)
+        p13, p2 = tsm.pack_moe_weights(w13, w2)
+        assert tuple(p13.shape) == (E, 2 * Ip, Hp) and tuple(p2.shape) == (E, Hp, Ip)
+        assert torch.equal(p13.cpu(), layout.pack(w13.cpu(), True, 2 * Ip, Hp)), (E, I, H)
+        assert torch.equal(p2.cpu(), layout.pack(w2.cpu(), False, Hp, Ip)), (E, I, H)
+        assert torch.equal(layout.unpack(p13, True, 2 * I, H), w13)
+        assert torch.equal(layout.unpack(p2, False, H, I), w2)
+
+
+@pytest.mark.parametrize("T", [1, 64, 700, 2048])
+def test_tp8_share_intermediate_96(dev, tsm, T):
+    """The one-GPU share of TP-8 for Qwen3-30B-A3B: I = 768 / 8 = 96, which the kernels run
+    zero-padded to 128 (the reference masks the ragged block instead, tinykernels.py:1719-1731).
+    Both the reference-layout op and the packed path against the oracle."""
+    from oracle.moe_oracle import make_layer
+    _, gw, w13, w2 = make_layer(1, 2048, 128, 96, torch.bfloat16, seed=5, device=dev)
+    x = xrand(T, 2048, dev, 500 + T)
+    w, ids, _ = tsm.moe_router(x, gw, 8, True)
+    out = tsm.fused_moe(x, w13, w2, w, ids)
+    p13, p2 = tsm.pack_moe_weights(w13, w2)
+    assert tuple(p2.shape) == (128, 2048, 128)
+    assert torch.equal(tsm.fused_moe_packed(x, p13, p2, w, ids), out)
+    assert torch.equal(tsm.moe_forward_packed(x, gw, p13, p2, 8, True), out)
+    rows = tsm.fused_moe(x, w13, w2, w, ids, sum_topk=False)
+    assert rows.shape == (T * 8, 2048)
+    sel = torch.arange(T) if T <= 700 else \
+        torch.randperm(T, generator=torch.Generator().manual_seed(T))[:512]
+    ref = moe_reference(x.cpu()[sel], w13.cpu(), w2.cpu(), w.cpu()[sel], ids.cpu().long()[sel])
+    assert_close(out.cpu()[sel], ref, f"I=96 T={T}")
+
+
+@pytest.mark.parametrize("T", [5, 300])
+def test_ragged_hidden_size(dev, tsm, T):
+    """H = 200 (not a multiple of 128) and I = 50: x is zero-padded to H_pad = 256 for the
+    experts and the output cut back to H; the router runs on the true H (padded to a multiple
+    of 8 with zero columns, which leaves its sums unchanged)."""
+    from oracle.moe_oracle import make_layer
+    E, k = 16, 4
+    x, gw, w13, w2 = make_layer(T, 200, E, 50, torch.bfloat16, seed=6, device=dev)
+    w, ids, logits = tsm.moe_router(x, gw, k, True)
+    bits = lambda t: t.contiguous().cpu().view(torch.int16).numpy().view(np.uint16)  # noqa: E731
+    ol = c_oracle.router_logits(bits(x), bits(gw))
+    assert np.array_equal(logits.cpu().numpy().view(np.uint32), ol.view(np.uint32))
+    out = tsm.moe_forward(x, gw, w13, w2, k, True)
+    assert out.shape == (T, 200)
+    ref = moe_reference(x.cpu(), w13.cpu(), w2.cpu(), w.cpu(), ids.cpu().long())
+    assert_close(out, ref, f"H=200 T={T}")
+    p13, p2 = tsm.pack_moe_weights(w13, w2)
+    assert torch.equal(tsm.moe_forward_packed(x, gw, p13, p2, k, True), out)
+
+
+def test_module_routes_like_bf16_linear(dev, tsm, qwen_layer):
+    """SparseMoE (bf16) routes on bf16-rounded logits, as serve.py's bf16 nn.Linear gate does
+    (serve.py:1079): its ids equal the oracle's selection on the bf16 logits of the module's own
+    router, and those logits agree with torch's bf16 Linear to within one bf16 ulp (the GEMM
+    libraries sum in another order, so a logit near a rounding boundary may round the other way).
+    The input is tie-prone: repeated token rows and a gate with duplicated expert rows."""
+    from types import SimpleNamespace
+    (gw, w13, w2), _ = qwen_layer
+    gw_t = gw.clone()
+    gw_t[1::2] = gw_t[0::2]                      # experts 2j and 2j+1 always tie
+    x = xrand(32, 2048, dev, 61).repeat(2, 1)
+    w, ids, logits = tsm.moe_router(x, gw_t, 8, True, None, None, True)
+    ow, oids = c_oracle.route(logits.cpu().numpy(), 8, True)
+    assert np.array_equal(ids.cpu().numpy(), oids)
+    assert np.array_equal(w.cpu().numpy().view(np.uint32), ow.view(np.uint32))
+    # ties resolve to the lower expert index
+    assert bool((ids.cpu()[:, 0] % 2 == 0).all())
+    lin = F.linear(x, gw_t).float()
+    d = (lin - logits).abs()
+    ulp = logits.abs().clamp_min(2.0 ** -126) * 2.0 ** -7
+    assert bool((d <= ulp).all())
+    assert (d > 0).float().mean().item() < 1e-2
+    cfg = SimpleNamespace(num_experts=128, hidden_size=2048, moe_intermediate_size=768,
+                          num_experts_per_tok=8, norm_topk_prob=True)
+    m = tsm.SparseMoE(cfg).to(device=dev, dtype=torch.bfloat16)
+    with torch.no_grad():
+        m.gate.weight.copy_(gw_t)
+        m.w13.copy_(w13)
+        m.w2.copy_(w2)
+        out = m(x)
+    assert torch.equal(out, tsm.fused_moe(x, w13, w2, w, ids))

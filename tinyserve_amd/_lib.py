@@ -42,6 +42,8 @@ def _load():
         "tsm_moe_expert_gate_up": ([P, P, P, I64, I32, I32, I32, I32, I32, P, P], I32),
         "tsm_moe_expert_down": ([P, P, P, P, I64, I32, I32, I32, I32, P, P], I32),
         "tsm_moe_pack_weights": ([P, I64, I32, I32, I32, P, P], I32),
+        "tsm_moe_padded_shape": ([I32, I32, P, P], I32),
+        "tsm_moe_pack_weights_padded": ([P, I64, I32, I32, I32, I32, I32, P, P], I32),
         "tsm_fused_moe_packed": ([P, P, P, P, P, I64, I32, I32, I32, I32, I32, P, P, SZ, P], I32),
         "tsm_moe_forward_packed": ([P, P, P, P, P, P, I64, I32, I32, I32, I32, I32, I32, I32, P, P,
                                     P, P, SZ, P], I32),

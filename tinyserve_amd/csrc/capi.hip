@@ -26,6 +26,14 @@ int check_launch(const char* what) {
     }
     return TSM_OK;
 }
+
+int launch_status(hipError_t e, const char* what) {
+    if (e != hipSuccess) {
+        set_error("%s: %s", what, hipGetErrorString(e));
+        return TSM_E_HIP;
+    }
+    return TSM_OK;
+}
 }  // namespace tsm
 
 extern "C" const char* tsm_last_error(void) { return tsm::g_error; }

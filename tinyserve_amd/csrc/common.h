@@ -143,6 +143,10 @@ namespace tsm {
 void set_error(const char* fmt, ...);
 void clear_error();
 int check_launch(const char* what);
+// Status of a launch helper that already collected hipGetLastError(): the stage's name goes into
+// the error message (a later check_launch would no longer see the error, which the first
+// hipGetLastError call cleared).
+int launch_status(hipError_t e, const char* what);
 }  // namespace tsm
 
 #define TSM_REQUIRE(cond, code, ...)          \

@@ -245,6 +245,7 @@ extern "C" int tsm_moe_align(const int32_t* ids, int64_t numel, int E, int block
     const size_t need = align_workspace_bytes(numel, E);
     TSM_REQUIRE(ws_bytes >= need && (need == 0 || ws != nullptr), TSM_E_WORKSPACE,
                 "align workspace too small: need %zu bytes, got %zu", need, ws_bytes);
-    (void)launch_align(ids, numel, E, block_m, sorted_ids, expert_ids, total, ws, stream);
-    return check_launch("align kernels");
+    return launch_status(
+        launch_align(ids, numel, E, block_m, sorted_ids, expert_ids, total, ws, stream),
+        "align kernels");
 }

@@ -426,6 +426,7 @@ bool launch_expert_stages(const bf16_t* x, const bf16_t* w13, const bf16_t* w2,
 int run_experts(const void* x, const void* w13, const void* w2, const float* topk_w,
                 const int32_t* topk_ids, int64_t T, int H, int I, int E, int top_k, int sum_topk,
                 bool packed, void* out, char* ws, const Layout& L, hipStream_t stream) {
+    int rc = TSM_OK;
     const Plan pl = plan_for(T, H, I, E, top_k, packed);
     const int64_t numel = T * top_k;
     bf16_t* rows = sum_topk ? reinterpret_cast<bf16_t*>(ws + L.rows) : (bf16_t*)out;
@@ -453,7 +454,10 @@ int run_experts(const void* x, const void* w13, const void* w2, const float* top
     int32_t* total = reinterpret_cast<int32_t*>(ws + L.total);
     bf16_t* act = reinterpret_cast<bf16_t*>(ws + L.act);
 
-    (void)launch_align(topk_ids, numel, E, pl.block_m, sorted, eids, total, ws + L.hist, stream);
+    rc = launch_status(
+        launch_align(topk_ids, numel, E, pl.block_m, sorted, eids, total, ws + L.hist, stream),
+        "fused_moe align kernels");
+    if (rc) return rc;
     launch_gate_up((const bf16_t*)x, (const bf16_t*)w13, sorted, eids, total, numel, top_k, H, I,
                    E, pl.block_m, packed, act, stream);
     launch_down(act, (const bf16_t*)w2, topk_w, sorted, eids, total, numel, H, I, E, pl.block_m,

@@ -697,6 +697,5 @@ extern "C" int tsm_moe_router(const void* x, const void* gate_w, int dtype, int6
         set_error("router dtype code %d not supported", dtype);
         return TSM_E_DTYPE;
     }
-    (void)err;
-    return check_launch("router_kernel");
+    return launch_status(err, "router kernels");
 }

@@ -10,6 +10,9 @@ from typing import Optional, Tuple
 import torch
 from torch import Tensor
 
+import ctypes
+import weakref
+
 from ._lib import TSM_BF16, TSM_F32, check, lib, ptr, stream_of
 
 
@@ -75,6 +78,11 @@ def moe_router(x: Tensor, gate_w: Tensor, top_k: int, renormalize: bool,
     E = gate_w.shape[0]
     if gate_w.shape[1] != H:
         raise ValueError(f"gate weight {tuple(gate_w.shape)} does not match x {tuple(x.shape)}")
+    if H % 8:
+        # the kernels read rows in 8-element chunks: zero columns add exact zeros to every
+        # partial sum, so the logits keep their bits
+        H = (H + 7) // 8 * 8
+        x, gate_w = _pad_cols(x, H), _pad_cols(gate_w, H)
     w = torch.empty(T, top_k, dtype=torch.float32, device=x.device)
     ids = torch.empty(T, top_k, dtype=torch.int32, device=x.device)
     logits = torch.empty(T, E, dtype=torch.float32, device=x.device)
@@ -155,6 +163,18 @@ def _(gate, up):
 
 
 # ---------------------------------------------------------------- experts
+def padded_shape(H: int, I: int) -> Tuple[int, int]:
+    """(H_pad, I_pad): the sizes the expert kernels run at (equal to (H, I) when the kernels
+    take those sizes; else rounded up, with the margin of the packed weights zero)."""
+    hp, ip = ctypes.c_int(0), ctypes.c_int(0)
+    check(lib.tsm_moe_padded_shape(H, I, ctypes.byref(hp), ctypes.byref(ip)), "padded_shape")
+    return hp.value, ip.value
+
+
+def _needs_padding(H: int, I: int) -> bool:
+    return padded_shape(H, I) != (H, I)
+
+
 def _check_weights(x, w13, w2):
     if x.dtype != torch.bfloat16 or w13.dtype != torch.bfloat16 or w2.dtype != torch.bfloat16:
         raise TypeError(f"fused_moe runs in bf16 (got x {x.dtype}, w13 {w13.dtype}, "
@@ -168,20 +188,68 @@ def _check_weights(x, w13, w2):
     return T, H, E, I
 
 
+def _check_packed(x, w13p, w2p):
+    """Packed weights may carry the padded sizes of padded_shape(H, I): w13p [E, 2 I_pad, H_pad],
+    w2p [E, H_pad, I_pad]. Returns (T, H, H_pad, E, I_pad)."""
+    if x.dtype != torch.bfloat16 or w13p.dtype != torch.bfloat16 or w2p.dtype != torch.bfloat16:
+        raise TypeError(f"fused_moe runs in bf16 (got x {x.dtype}, w13 {w13p.dtype}, "
+                        f"w2 {w2p.dtype})")
+    T, H = x.shape
+    E, two_i, Hp = w13p.shape
+    Ip = two_i // 2
+    if tuple(w2p.shape) != (E, Hp, Ip) or two_i != 2 * Ip:
+        raise ValueError(f"packed weight shapes w13 {tuple(w13p.shape)} / w2 {tuple(w2p.shape)} "
+                         f"are inconsistent")
+    if Hp != H and padded_shape(H, Ip)[0] != Hp:
+        raise ValueError(f"packed weights have H={Hp}, which is neither x's H={H} nor its "
+                         f"padded size {padded_shape(H, Ip)[0]}")
+    return T, H, Hp, E, Ip
+
+
+def _pad_cols(x, n):
+    return x if x.shape[1] == n else torch.nn.functional.pad(x, (0, n - x.shape[1]))
+
+
 def _fused_moe_impl(x, w13, w2, topk_weights, topk_ids, sum_topk, packed):
     _on_gpu(x, w13, w2, topk_weights, topk_ids)
     x, w13, w2 = _contig(x), _contig(w13), _contig(w2)
-    T, H, E, I = _check_weights(x, w13, w2)
+    if not packed:
+        T, H, E, I = _check_weights(x, w13, w2)
+        if _needs_padding(H, I):
+            # a shape the kernels do not take as it is: run on a zero-padded packed copy
+            w13, w2 = _padded_pack_cached(w13, w2)
+            packed = True
+    if packed:
+        T, H, Hp, E, Ip = _check_packed(x, w13, w2)
+    else:
+        Hp, Ip = H, I
     k = topk_ids.shape[1]
     tw = _contig(topk_weights.to(torch.float32))
     ti = _contig(topk_ids.to(torch.int32))
-    out = torch.empty((T, H) if sum_topk else (T * k, H), dtype=x.dtype, device=x.device)
-    nws = int(lib.tsm_fused_moe_workspace_size(T, H, I, E, k))
+    xp = _pad_cols(x, Hp)
+    out = torch.empty((T, Hp) if sum_topk else (T * k, Hp), dtype=x.dtype, device=x.device)
+    nws = int(lib.tsm_fused_moe_workspace_size(T, Hp, Ip, E, k))
     ws = torch.empty(max(nws, 1), dtype=torch.uint8, device=x.device)
     fn = lib.tsm_fused_moe_packed if packed else lib.tsm_fused_moe
-    check(fn(ptr(x), ptr(w13), ptr(w2), ptr(tw), ptr(ti), T, H, I, E, k, int(sum_topk), ptr(out),
-             ptr(ws), nws, stream_of(x)), "fused_moe")
-    return out
+    check(fn(ptr(xp), ptr(w13), ptr(w2), ptr(tw), ptr(ti), T, Hp, Ip, E, k, int(sum_topk),
+             ptr(out), ptr(ws), nws, stream_of(x)), "fused_moe")
+    return out if Hp == H else out[:, :H].contiguous()
+
+
+# Zero-padded packed copies made for reference-layout weights whose shape the kernels do not take
+# as it is, one per weight tensor (dropped with it), rebuilt when its version counter moves.
+_padded_cache: "weakref.WeakKeyDictionary" = weakref.WeakKeyDictionary()
+
+
+def _padded_pack_cached(w13, w2):
+    key = (w2.data_ptr(), w13._version, w2._version)
+    hit = _padded_cache.get(w13)
+    if hit is not None and hit[0] == key:
+        return hit[1]
+    with torch.no_grad():
+        p = pack_moe_weights(w13, w2)
+    _padded_cache[w13] = (key, p)
+    return p
 
 
 @torch.library.custom_op("tinyserve_amd::fused_moe", mutates_args=())
@@ -214,42 +282,60 @@ def _(x, w13_packed, w2_packed, topk_weights, topk_ids, sum_topk=True):
 
 @torch.library.custom_op("tinyserve_amd::pack_moe_weights", mutates_args=())
 def pack_moe_weights(w13: Tensor, w2: Tensor) -> Tuple[Tensor, Tensor]:
-    """MFMA-tiled copies of w13 [E, 2I, H] and w2 [E, H, I] (same shapes and sizes); one-time,
-    at weight-load time. Their contents are only meaningful to the *_packed ops."""
+    """MFMA-tiled copies of w13 [E, 2I, H] and w2 [E, H, I]; one-time, at weight-load time. Same
+    shapes when the kernels take (H, I) as they are; otherwise [E, 2 I_pad, H_pad] and
+    [E, H_pad, I_pad] (padded_shape) with a zero margin. Their contents are only meaningful to
+    the *_packed ops."""
     _on_gpu(w13, w2)
     if w13.dtype != torch.bfloat16 or w2.dtype != torch.bfloat16:
         raise TypeError("packing supports bf16 weights")
     w13, w2 = _contig(w13), _contig(w2)
     E, two_i, H = w13.shape
     I = two_i // 2
-    if tuple(w2.shape) != (E, H, I):
+    if tuple(w2.shape) != (E, H, I) or two_i != 2 * I:
         raise ValueError(f"w2 {tuple(w2.shape)} does not match w13 {tuple(w13.shape)}")
-    p13, p2 = torch.empty_like(w13), torch.empty_like(w2)
+    Hp, Ip = padded_shape(H, I)
+    p13 = torch.empty(E, 2 * Ip, Hp, dtype=w13.dtype, device=w13.device)
+    p2 = torch.empty(E, Hp, Ip, dtype=w2.dtype, device=w2.device)
     s = stream_of(w13)
-    check(lib.tsm_moe_pack_weights(ptr(w13), E, two_i, H, 1, ptr(p13), s), "pack w13")
-    check(lib.tsm_moe_pack_weights(ptr(w2), E, H, I, 0, ptr(p2), s), "pack w2")
+    check(lib.tsm_moe_pack_weights_padded(ptr(w13), E, two_i, H, 2 * Ip, Hp, 1, ptr(p13), s),
+          "pack w13")
+    check(lib.tsm_moe_pack_weights_padded(ptr(w2), E, H, I, Hp, Ip, 0, ptr(p2), s), "pack w2")
     return p13, p2
 
 
 @pack_moe_weights.register_fake
 def _(w13, w2):
-    return torch.empty_like(w13), torch.empty_like(w2)
+    E, two_i, H = w13.shape
+    Hp, Ip = padded_shape(H, two_i // 2)
+    return w13.new_empty(E, 2 * Ip, Hp), w2.new_empty(E, Hp, Ip)
 
 
 def _moe_forward_impl(x, gate_w, w13, w2, top_k, renormalize, expert_map, bias, logits_bf16,
                       sum_topk, packed):
     _on_gpu(x, gate_w, w13, w2, expert_map, bias)
     x, gate_w, w13, w2 = _contig(x), _contig(gate_w), _contig(w13), _contig(w2)
-    T, H, E, I = _check_weights(x, w13, w2)
+    if packed:
+        T, H, Hp, E, Ip = _check_packed(x, w13, w2)
+        ragged = Hp != H
+    else:
+        T, H, E, I = _check_weights(x, w13, w2)
+        ragged = _needs_padding(H, I)
     if gate_w.dtype != torch.bfloat16 or tuple(gate_w.shape) != (E, H):
         raise ValueError(f"gate weight must be bf16 [E, H] = [{E}, {H}]")
+    if ragged:
+        # router on the true hidden size, experts on the padded one
+        w, ids, _ = moe_router(x, gate_w, top_k, renormalize, expert_map, bias, logits_bf16)
+        return _fused_moe_impl(x, w13, w2, w, ids, sum_topk, packed)
+    if not packed:
+        Ip = I
     m = _map_arg(expert_map, x.device)
     b = None if bias is None else _contig(bias.to(device=x.device, dtype=torch.float32))
     out = torch.empty((T, H) if sum_topk else (T * top_k, H), dtype=x.dtype, device=x.device)
-    nws = int(lib.tsm_moe_forward_workspace_size(T, H, I, E, top_k))
+    nws = int(lib.tsm_moe_forward_workspace_size(T, H, Ip, E, top_k))
     ws = torch.empty(max(nws, 1), dtype=torch.uint8, device=x.device)
     fn = lib.tsm_moe_forward_packed if packed else lib.tsm_moe_forward
-    check(fn(ptr(x), ptr(gate_w), ptr(w13), ptr(w2), ptr(m), ptr(b), T, H, I, E, top_k,
+    check(fn(ptr(x), ptr(gate_w), ptr(w13), ptr(w2), ptr(m), ptr(b), T, H, Ip, E, top_k,
              int(renormalize), int(logits_bf16), int(sum_topk), ptr(out), None, None, ptr(ws),
              nws, stream_of(x)), "moe_forward")
     return out
