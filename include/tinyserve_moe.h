@@ -178,6 +178,24 @@ int tsm_moe_forward(const void* x, const void* gate_w, const void* w13, const vo
                     hipStream_t stream);
 
 /*
+ * Residual-add RMSNorm, optionally fused with the MoE block's top-k combine.
+ * Replaces the decoder's add_rmsnorm (serve.py:1177-1193) over tinykernels.rmsnorm /
+ * _rmsnorm_kernel (tinykernels.py:26-105) and, with top_k > 1, also the k-sum of fused_moe
+ * (tinykernels.py:1796) that produced its input.
+ * x: [T*top_k, H] bf16 (top_k = 1: the [T, H] input itself; top_k > 1: the per-slot rows of
+ * tsm_fused_moe with sum_topk = 0). Per token t:
+ *   s = bf16(sum_{j<top_k} x[t*top_k + j])            (fp32, slot order; top_k = 1: x[t])
+ *   if residual_in: s = bf16(float(s) + float(residual[t]))
+ *   if residual:    residual[t] = s                    (in place; [T, H] bf16)
+ *   out[t] = bf16(float(s) * rsqrt(mean(float(s)^2) + eps) * float(weight))
+ * The sum of squares is taken in a fixed order (deterministic). residual may be null when
+ * residual_in == 0 (plain RMSNorm). out must not alias x or residual. Requires H % 8 == 0,
+ * 8 <= H <= 16384, 1 <= top_k <= 64.
+ */
+int tsm_add_rmsnorm(const void* x, int64_t T, int H, int top_k, void* residual, int residual_in,
+                    const void* weight, float eps, void* out, hipStream_t stream);
+
+/*
  * MFMA-tiled ("packed") expert weights. No counterpart in the reference, which streams w13/w2 in
  * their checkpoint layout (tinykernels.py:1707-1738); this is a one-time reordering (same size)
  * after which every 16x16x32 MFMA operand of a 16-row block is 1 KiB of contiguous memory:

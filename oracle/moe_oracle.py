@@ -14,6 +14,10 @@ Functions and the reference code they restate:
 - moe_align_block_size_np  tinykernels.py:1070-1190 (the torch moe_align_block_size).
 - sparse_moe_reference     serve.py:1076-1099 at TP=1 with TRITON_KERNELS off: gate Linear, route,
                                               moe_reference.
+- add_rmsnorm_reference    serve.py:799-809 (RMSNorm, fp32) and 1185-1193 (add_rmsnorm: residual
+                                              = residual + x in bf16, then the norm), with x the
+                                              k-sum of the per-slot rows as tinykernels.py:1796
+                                              forms it (fp32 sum in slot order, rounded once).
 - per_token_fp64           textbook formula sum_k w_k * W2_e (silu(W1_e x) * W3_e x) in float64,
                            used only to pin moe_reference itself.
 """
@@ -98,6 +102,20 @@ def moe_align_block_size_np(topk_ids, block_m, num_experts):
     expert_ids = np.where(expert_ids >= num_experts, -1, expert_ids).astype(np.int32)
     total = np.array([padded_end[-1] if nb else 0], dtype=np.int32)
     return sorted_ids, expert_ids, total
+
+
+def add_rmsnorm_reference(rows, top_k, residual, weight, eps):
+    """rows [T*k, H] (k = 1: x [T, H]); residual [T, H] or None. Returns (out, new_residual)."""
+    H = rows.shape[-1]
+    r = rows.reshape(-1, top_k, H).float()
+    s = r[:, 0]
+    for j in range(1, top_k):           # slot order, fp32, one rounding at the end
+        s = s + r[:, j]
+    x = s.to(torch.bfloat16)
+    res = x if residual is None else (residual.reshape(-1, H) + x)   # bf16 add (serve.py:1192)
+    xf = res.float()
+    out = (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps) * weight.float())
+    return out.to(torch.bfloat16), res
 
 
 def per_token_fp64(x, w13, w2, topk_weights, topk_ids):

@@ -72,3 +72,31 @@ def test_invalid_arguments_return_codes(lib):
              16, None) == -4                                                     # workspace
     assert b"workspace" in lib.tsm_last_error()
     assert g(None, None, None, None, None, 0, 2048, 768, 128, 8, 1, None, None, 0, None) == 0
+
+
+def test_padded_shape_and_norm_validation(lib):
+    P, I64, I32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
+    lib.tsm_last_error.restype = ctypes.c_char_p
+    ps = lib.tsm_moe_padded_shape
+    ps.argtypes = [I32, I32, P, P]
+    hp, ip = ctypes.c_int(), ctypes.c_int()
+    for (H, I), want in {(2048, 768): (2048, 768), (2048, 96): (2048, 128),
+                         (200, 50): (256, 128), (2048, 192): (2048, 192)}.items():
+        assert ps(H, I, ctypes.byref(hp), ctypes.byref(ip)) == 0
+        assert (hp.value, ip.value) == want
+    assert ps(0, 96, ctypes.byref(hp), ctypes.byref(ip)) == -1
+    pk = lib.tsm_moe_pack_weights_padded
+    pk.argtypes = [P, I64, I32, I32, I32, I32, I32, P, P]
+    assert pk(P(256), 2, 192, 2048, 200, 2048, 1, P(512), None) == -2   # N_pad % 32 (interleaved)
+    assert pk(P(256), 2, 192, 2048, 128, 2048, 1, P(512), None) == -2   # N_pad < N
+    assert pk(P(256), 2, 2048, 96, 2048, 100, 0, P(512), None) == -2    # K_pad % 32
+    assert pk(P(256), 2, 2048, 96, 2048, 128, 0, P(256), None) == -1    # in place
+    nf = lib.tsm_add_rmsnorm
+    nf.argtypes = [P, I64, I32, I32, P, I32, P, ctypes.c_float, P, P]
+    assert nf(P(256), 4, 100, 1, None, 0, P(256), 1e-6, P(512), None) == -2     # H % 8
+    assert nf(P(256), 4, 32768, 1, None, 0, P(256), 1e-6, P(512), None) == -2   # H too large
+    assert nf(P(256), 4, 2048, 0, None, 0, P(256), 1e-6, P(512), None) == -1    # top_k
+    assert nf(P(256), 4, 2048, 8, None, 1, P(256), 1e-6, P(512), None) == -1    # no residual
+    assert b"residual" in lib.tsm_last_error()
+    assert nf(None, 4, 2048, 8, None, 0, P(256), 1e-6, P(512), None) == -1      # null x
+    assert nf(None, 0, 2048, 8, None, 0, None, 1e-6, None, None) == 0           # empty batch

@@ -217,3 +217,44 @@ def test_bf16_rounding_points_of_reference():
     assert err.max() < 2e-2 and (err.mean() / ref.abs().mean()) < 5e-3
     gu = x[:1] @ w13[0].t()
     assert torch.equal(F.silu(gu[:, :512]), F.silu(gu[:, :512].float()).bfloat16())
+
+
+# ---------------------------------------------------------------- residual-add RMSNorm
+def _bf16_ulp(v):
+    return torch.exp2(torch.floor(torch.log2(v.abs().clamp_min(2.0 ** -126))) - 7)
+
+
+@pytest.mark.parametrize("k,with_res", [(1, False), (1, True), (8, True), (2, False)])
+def test_add_rmsnorm_reference_against_fp64(k, with_res):
+    from oracle.moe_oracle import add_rmsnorm_reference
+    g = torch.Generator().manual_seed(k * 10 + with_res)
+    T, H, eps = 7, 256, 1e-6
+    rows = (torch.randn(T * k, H, generator=g) * 0.5).bfloat16()
+    res = (torch.randn(T, H, generator=g) * 2).bfloat16() if with_res else None
+    w = (1 + 0.1 * torch.randn(H, generator=g)).bfloat16()
+    out, new_res = add_rmsnorm_reference(rows, k, res, w, eps)
+    # the k-sum: float64 sum rounded to bf16, within one rounding of it
+    s64 = rows.double().view(T, k, H).sum(1)
+    x = s64.to(torch.bfloat16)
+    assert bool(((new_res.double() - (x.double() if res is None else
+                                      (x.double() + res.double()))).abs()
+                 <= _bf16_ulp(new_res.double()) * (1 if res is None else 2)).all())
+    if res is not None and k == 1:   # one bf16 rounding of the fp32 sum of the two bf16 inputs
+        assert torch.equal(new_res, (rows.float() + res.float()).bfloat16())
+    r = new_res.double()
+    ref = r / torch.sqrt((r * r).mean(-1, keepdim=True) + eps) * w.double()
+    assert bool(((out.double() - ref).abs() <= _bf16_ulp(ref) + 1e-30).all())
+
+
+def test_add_rmsnorm_reference_known_answers():
+    from oracle.moe_oracle import add_rmsnorm_reference
+    H = 64
+    w = torch.linspace(0.5, 2.0, H).bfloat16()
+    rows = torch.full((3, H), -4.0).bfloat16()          # constant row: x / rms(x) = sign(x)
+    out, res = add_rmsnorm_reference(rows, 1, None, w, 0.0)
+    assert torch.equal(out, (-w.float()).bfloat16().expand(3, H))
+    assert torch.equal(res, rows)
+    # rows of two slots that cancel, plus a residual of ones: the norm sees the residual alone
+    rows2 = torch.stack([torch.full((H,), 3.0), torch.full((H,), -3.0)]).bfloat16()
+    out, res = add_rmsnorm_reference(rows2, 2, torch.ones(1, H).bfloat16(), w, 0.0)
+    assert torch.equal(res, torch.ones(1, H).bfloat16()) and torch.equal(out[0], w)

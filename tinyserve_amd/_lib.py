@@ -48,6 +48,7 @@ def _load():
         "tsm_moe_forward_packed": ([P, P, P, P, P, P, I64, I32, I32, I32, I32, I32, I32, I32, P, P,
                                     P, P, SZ, P], I32),
         "tsm_moe_combine": ([P, I64, I32, I32, P, P], I32),
+        "tsm_add_rmsnorm": ([P, I64, I32, I32, P, I32, P, ctypes.c_float, P, P], I32),
         "tsm_moe_forward_workspace_size": ([I64, I32, I32, I32, I32], SZ),
         "tsm_moe_forward": ([P, P, P, P, P, P, I64, I32, I32, I32, I32, I32, I32, I32, P, P, P,
                              P, SZ, P], I32),

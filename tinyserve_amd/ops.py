@@ -373,3 +373,55 @@ def _(x, gate_w, w13_packed, w2_packed, top_k, renormalize, expert_map=None, bia
       logits_bf16=False, sum_topk=True):
     T, H = x.shape
     return x.new_empty((T, H) if sum_topk else (T * top_k, H))
+
+
+# ---------------------------------------------------------------- residual-add RMSNorm
+def _norm_impl(x, top_k, residual, residual_in, weight, eps):
+    _on_gpu(x, residual, weight)
+    if x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
+        raise TypeError(f"add_rmsnorm runs in bf16 (got x {x.dtype}, weight {weight.dtype})")
+    H = x.shape[-1]
+    x2 = _contig(x.reshape(-1, H))
+    if x2.shape[0] % top_k:
+        raise ValueError(f"{x2.shape[0]} rows are not a whole number of tokens of {top_k} slots")
+    T = x2.shape[0] // top_k
+    if tuple(weight.shape) != (H,):
+        raise ValueError(f"weight {tuple(weight.shape)} does not match H={H}")
+    if residual is not None and (residual.dtype != torch.bfloat16 or residual.numel() != T * H
+                                 or not residual.is_contiguous()):
+        raise ValueError("residual must be a contiguous bf16 tensor of T*H elements")
+    out = torch.empty(T, H, dtype=x.dtype, device=x.device)
+    check(lib.tsm_add_rmsnorm(ptr(x2), T, H, top_k, ptr(residual), int(residual_in),
+                              ptr(_contig(weight)), float(eps), ptr(out), stream_of(x2)),
+          "add_rmsnorm")
+    return out
+
+
+@torch.library.custom_op("tinyserve_amd::rmsnorm", mutates_args=("residual",))
+def rmsnorm(x: Tensor, weight: Tensor, eps: float,
+            residual: Optional[Tensor] = None) -> Tensor:
+    """tinykernels.rmsnorm (tinykernels.py:63-105): out = rmsnorm(x) * weight, or with a residual
+    `residual += x` (rounded to bf16) then out = rmsnorm(residual) * weight, in one launch."""
+    return _norm_impl(x, 1, residual, residual is not None, weight, eps).view(x.shape)
+
+
+@rmsnorm.register_fake
+def _(x, weight, eps, residual=None):
+    return torch.empty_like(x)
+
+
+@torch.library.custom_op("tinyserve_amd::moe_combine_add_rmsnorm", mutates_args=("residual",))
+def moe_combine_add_rmsnorm(rows: Tensor, top_k: int, residual: Tensor, weight: Tensor,
+                            eps: float, residual_in: bool = True) -> Tensor:
+    """The MoE block's k-sum fused into the next residual-add RMSNorm: rows [T*k, H] (fused_moe
+    with sum_topk=False) -> residual = bf16(bf16(sum_k rows) + residual) (residual_in; else
+    residual = bf16(sum_k rows)), returns rmsnorm(residual) * weight [T, H]."""
+    if residual is None:
+        raise ValueError("moe_combine_add_rmsnorm needs a residual buffer")
+    return _norm_impl(rows, top_k, residual, residual_in, weight, eps)
+
+
+@moe_combine_add_rmsnorm.register_fake
+def _(rows, top_k, residual, weight, eps, residual_in=True):
+    H = rows.shape[-1]
+    return rows.new_empty(rows.numel() // H // top_k, H)
