@@ -548,6 +548,125 @@ __global__ __launch_bounds__(kTileWaves * 64) void router_tile_kernel(
     }
 }
 
+// Prefill-sized batches (T > 256, bf16, E <= 128): the gate GEMM on the matrix cores. A
+// workgroup of 8 wavefronts owns 64 tokens x all experts; wavefront (wm, wn) computes tokens
+// 16 wm .. 16 wm + 15 against experts 64 wn .. 64 wn + 63 with 16x16x32 bf16 MFMAs (fp32
+// accumulation), its operands read straight from the row-major x and gate matrices (an MFMA
+// operand of a 16-row block is 16 rows x 64 bytes, one 16-byte load per lane), the next k-step's
+// operands requested before the current step's MFMAs. The logits go through LDS, are written
+// to logits_out (if given) in row order, and each wavefront then routes 8 of the tokens with
+// wave_select, the selection every router path uses.
+// The MFMA accumulation order is the hardware's, not the fixed order of the other router
+// kernels: logits agree with the exact dot products to fp32 accumulation accuracy, and the ids
+// and weights are those of the fixed-order selection applied to these logits.
+constexpr int kMfmaTokens = 64;
+constexpr int kMfmaWaves = 8;
+constexpr int kMfmaLd = 128 + 4;  // LDS row stride of the logits tile (floats)
+constexpr int kRouterDepth = 4;   // k-steps of operands in flight per wavefront
+
+__global__ __launch_bounds__(kMfmaWaves * 64) void router_mfma_kernel(
+    const bf16_t* __restrict__ x, const bf16_t* __restrict__ gw, int64_t T, int H, int E,
+    int top_k, int renorm, const int64_t* __restrict__ expert_map, const float* __restrict__ bias,
+    int logits_bf16, float* __restrict__ logits_out, float* __restrict__ topk_w,
+    int32_t* __restrict__ topk_ids) {
+#pragma clang fp contract(off)
+    __shared__ float s_log[kMfmaTokens * kMfmaLd];
+    __shared__ __attribute__((aligned(16))) uint32_t s_sel[kMfmaWaves][kSelectLds];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int64_t t0 = (int64_t)blockIdx.x * kMfmaTokens;
+
+    // operand rows, clamped into range (rows past T or E are computed and never used)
+    const int64_t arow = min(t0 + wm * 16 + (lane & 15), T - 1);
+    const u32x4* ap = reinterpret_cast<const u32x4*>(x + arow * H + (lane >> 4) * 8);
+    const u32x4* bp[4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        const int erow = min(wn * 64 + g * 16 + (lane & 15), E - 1);
+        bp[g] = reinterpret_cast<const u32x4*>(gw + (int64_t)erow * H + (lane >> 4) * 8);
+    }
+    f32x4 acc[4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) acc[g] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // k-steps of 32; one step advances each operand pointer by 32 bf16 (4 x 16 bytes). The
+    // operands of kDepth - 1 steps are in flight while a step's MFMAs run (slot s % kDepth);
+    // KS is a multiple of kDepth, and the loads past the last step re-read it (unused), so every
+    // step issues the same loads and the waits count them exactly.
+    const int KS = H / 32;
+    u32x4 a[kRouterDepth], b[kRouterDepth][4];
+    auto load = [&](int slot_s, int step) {
+        step = min(step, KS - 1);
+        a[slot_s] = ap[step * 4];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) b[slot_s][g] = bp[g][step * 4];
+    };
+#pragma unroll
+    for (int d = 0; d + 1 < kRouterDepth; ++d) load(d, d);
+    for (int s0 = 0; s0 < KS; s0 += kRouterDepth) {
+#pragma unroll
+        for (int d = 0; d < kRouterDepth; ++d) {
+            load((d + kRouterDepth - 1) % kRouterDepth, s0 + d + kRouterDepth - 1);
+            // keep the loads ahead of this step's MFMAs (the scheduler would otherwise sink
+            // them next to their uses and shorten the pipeline)
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+                acc[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                    as_bf16x8(a[d]), as_bf16x8(b[d][g]), acc[g], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    // element i of block g: token 16 wm + 4 (lane / 16) + i, expert 64 wn + 16 g + lane % 16
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        const int e = wn * 64 + g * 16 + (lane & 15);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float l = acc[g][i];
+            if (bias && e < E) l = l + bias[e];
+            if (logits_bf16) l = round_bf16(l);
+            s_log[(wm * 16 + (lane >> 4) * 4 + i) * kMfmaLd + e] = l;
+        }
+    }
+    __syncthreads();
+    if (logits_out) {
+        for (int idx = tid; idx < kMfmaTokens * E; idx += kMfmaWaves * 64) {
+            const int tl = idx / E, e = idx - tl * E;
+            if (t0 + tl < T) logits_out[(t0 + tl) * E + e] = s_log[tl * kMfmaLd + e];
+        }
+    }
+    constexpr int kPerWave = kMfmaTokens / kMfmaWaves;
+    for (int j = 0; j < kPerWave; ++j) {
+        const int tl = wave * kPerWave + j;
+        const int64_t t = t0 + tl;
+        if (t >= T) break;  // uniform across the wavefront
+        float v[kMaxM];
+#pragma unroll
+        for (int q = 0; q < kMaxM; ++q) {
+            const int e = lane + 64 * q;
+            v[q] = (q < 2 && e < E) ? s_log[tl * kMfmaLd + e] : 0.0f;
+        }
+        wave_select(v, E, top_k, renorm, expert_map, topk_w + t * top_k, topk_ids + t * top_k,
+                    s_sel[wave]);
+    }
+}
+
+bool router_mfma_supported(int64_t T, int H, int E) {
+    return T > 256 && E >= 1 && E <= 128 && H >= 32 * kRouterDepth &&
+           H % (32 * kRouterDepth) == 0;
+}
+
+hipError_t launch_router_mfma(const void* x, const void* gw, int64_t T, int H, int E, int top_k,
+                              int renorm, const int64_t* expert_map, const float* bias,
+                              int logits_bf16, float* logits_out, float* w, int32_t* ids,
+                              hipStream_t stream) {
+    const int64_t blocks = (T + kMfmaTokens - 1) / kMfmaTokens;
+    hipLaunchKernelGGL(router_mfma_kernel, dim3((unsigned)blocks), dim3(kMfmaWaves * 64), 0,
+                       stream, (const bf16_t*)x, (const bf16_t*)gw, T, H, E, top_k, renorm,
+                       expert_map, bias, logits_bf16, logits_out, w, ids);
+    return hipGetLastError();
+}
+
 template <typename TIn, int NC>
 hipError_t launch_router_tile(const void* x, const void* gw, int64_t T, int H, int E, int top_k,
                               int renorm, const int64_t* expert_map, const float* bias,
@@ -687,7 +806,10 @@ extern "C" int tsm_moe_router(const void* x, const void* gate_w, int dtype, int6
     if (T == 0) return TSM_OK;
     TSM_REQUIRE(x && gate_w && topk_w && topk_ids, TSM_E_ARG, "null pointer argument");
     hipError_t err;
-    if (dtype == TSM_BF16)
+    if (dtype == TSM_BF16 && router_mfma_supported(T, H, E))
+        err = launch_router_mfma(x, gate_w, T, H, E, top_k, renorm, expert_map, bias,
+                                 logits_bf16, logits_out, topk_w, topk_ids, stream);
+    else if (dtype == TSM_BF16)
         err = launch_router<bf16_t>(x, gate_w, T, H, E, top_k, renorm, expert_map, bias,
                                     logits_bf16, logits_out, topk_w, topk_ids, stream);
     else if (dtype == TSM_F32)
