@@ -151,6 +151,18 @@ int tsm_moe_gemm_down(const void* act, const void* w2, const float* topk_w,
 int tsm_moe_combine(const void* rows, int64_t T, int H, int top_k, void* out, hipStream_t stream);
 
 /*
+ * tsm_fused_moe for fp32 activations and weights (same layouts, fp32 elements): every
+ * intermediate in fp32, as the reference's fused_moe keeps them in x.dtype (tinykernels.py:1784-
+ * 1791) and moe_reference computes an fp32 layer (serve.py:933-996): act = silu(x W1^T) * (x W3^T),
+ * rows = (act W2^T) * topk_w, out = fixed-order fp32 k-sum. Runs on the vector ALUs (16-row
+ * expert tiles of the align step); for the tiny fp32 configuration, not for throughput. Any H, I.
+ */
+size_t tsm_fused_moe_f32_workspace_size(int64_t T, int H, int I, int E, int top_k);
+int tsm_fused_moe_f32(const float* x, const float* w13, const float* w2, const float* topk_w,
+                      const int32_t* topk_ids, int64_t T, int H, int I, int E, int top_k,
+                      int sum_topk, float* out, void* ws, size_t ws_bytes, hipStream_t stream);
+
+/*
  * Expert-major stages used by fused_moe for decode-sized batches (tsm_moe_block_m() == 0): no
  * permutation step; each workgroup finds its expert's assignments by scanning topk_ids [numel]
  * (stable flat order, as moe_align_block_size orders them), and act [numel, I] holds the

@@ -406,3 +406,33 @@ def test_module_routes_like_bf16_linear(dev, tsm, qwen_layer):
         m.w2.copy_(w2)
         out = m(x)
     assert torch.equal(out, tsm.fused_moe(x, w13, w2, w, ids))
+
+
+@pytest.mark.parametrize("T", [64, 1, 300])
+def test_tiny_config_fp32(dev, tsm, T):
+    """Config 1 as specified: H=256, E=8, top-2, I=512, fp32 throughout (x ~ N(0,1), weights
+    ~ N(0, 0.02), seed 0): the fp32 router and the fp32 experts against the fp32 oracle (same
+    routing) and the float64 per-token formula."""
+    from types import SimpleNamespace
+    from oracle.moe_oracle import make_layer, per_token_fp64, route_torch
+    x, gw, w13, w2 = make_layer(T, 256, 8, 512, torch.float32, seed=0, device=dev)
+    w, ids, logits = tsm.moe_router(x, gw, 2, True)
+    rw, rids = route_torch(logits.cpu(), 2, True)
+    assert torch.equal(ids.cpu().long(), rids)
+    out = tsm.fused_moe(x, w13, w2, w, ids)
+    assert out.dtype == torch.float32
+    ref = moe_reference(x.cpu(), w13.cpu(), w2.cpu(), w.cpu(), ids.cpu().long())
+    assert torch.allclose(out.cpu(), ref, atol=2e-6, rtol=1e-4), (out.cpu() - ref).abs().max()
+    r64 = per_token_fp64(x.cpu(), w13.cpu(), w2.cpu(), w.cpu(), ids.cpu().long())
+    assert torch.allclose(out.cpu().double(), r64, atol=2e-6, rtol=1e-4)
+    rows = tsm.fused_moe(x, w13, w2, w, ids, sum_topk=False)
+    assert torch.equal(rows.view(T, 2, 256)[:, 0] + rows.view(T, 2, 256)[:, 1], out)
+    assert torch.equal(tsm.moe_forward(x, gw, w13, w2, 2, True), out)
+    cfg = SimpleNamespace(num_experts=8, hidden_size=256, moe_intermediate_size=512,
+                          num_experts_per_tok=2, norm_topk_prob=True)
+    m = tsm.SparseMoE(cfg).to(dev)
+    with torch.no_grad():
+        m.gate.weight.copy_(gw)
+        m.w13.copy_(w13)
+        m.w2.copy_(w2)
+        assert torch.equal(m(x), out)

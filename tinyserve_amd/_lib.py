@@ -37,6 +37,8 @@ def _load():
         "tsm_moe_block_m": ([I64, I32, I32, I32, I32, I32], I32),
         "tsm_fused_moe_workspace_size": ([I64, I32, I32, I32, I32], SZ),
         "tsm_fused_moe": ([P, P, P, P, P, I64, I32, I32, I32, I32, I32, P, P, SZ, P], I32),
+        "tsm_fused_moe_f32_workspace_size": ([I64, I32, I32, I32, I32], SZ),
+        "tsm_fused_moe_f32": ([P, P, P, P, P, I64, I32, I32, I32, I32, I32, P, P, SZ, P], I32),
         "tsm_moe_gemm_gate_up": ([P, P, P, P, P, I64, I32, I32, I32, I32, I32, I32, P, P], I32),
         "tsm_moe_gemm_down": ([P, P, P, P, P, P, I64, I32, I32, I32, I32, I32, P, P], I32),
         "tsm_moe_expert_gate_up": ([P, P, P, I64, I32, I32, I32, I32, I32, P, P], I32),

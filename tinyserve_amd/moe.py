@@ -179,7 +179,8 @@ class SparseMoE(nn.Module):
         return self.router_logits == "model" and self.gate.weight.dtype == torch.bfloat16
 
     def forward(self, x):
-        if self.packed:
+        # the packed layout is for the bf16 matrix-core kernels; fp32 layers run unpacked
+        if self.packed and (self.weights_packed or self.w13.dtype == torch.bfloat16):
             w13, w2 = self.pack()
             if self.router == "fused":
                 return ops.moe_forward_packed(x, self.gate.weight, w13, w2, self.top_k,

@@ -177,8 +177,8 @@ def _needs_padding(H: int, I: int) -> bool:
 
 def _check_weights(x, w13, w2):
     if x.dtype != torch.bfloat16 or w13.dtype != torch.bfloat16 or w2.dtype != torch.bfloat16:
-        raise TypeError(f"fused_moe runs in bf16 (got x {x.dtype}, w13 {w13.dtype}, "
-                        f"w2 {w2.dtype})")
+        raise TypeError(f"fused_moe runs in bf16, or fp32 in the reference layout (got x "
+                        f"{x.dtype}, w13 {w13.dtype}, w2 {w2.dtype})")
     T, H = x.shape
     E, two_i, H1 = w13.shape
     I = two_i // 2
@@ -210,9 +210,32 @@ def _pad_cols(x, n):
     return x if x.shape[1] == n else torch.nn.functional.pad(x, (0, n - x.shape[1]))
 
 
+def _fused_moe_f32(x, w13, w2, topk_weights, topk_ids, sum_topk):
+    """fp32 layer: every intermediate in fp32 (the reference keeps them in x.dtype)."""
+    T, H = x.shape
+    E, two_i, H1 = w13.shape
+    I = two_i // 2
+    if H1 != H or tuple(w2.shape) != (E, H, I) or two_i != 2 * I:
+        raise ValueError(f"weight shapes w13 {tuple(w13.shape)} / w2 {tuple(w2.shape)} do not "
+                         f"match x {tuple(x.shape)}")
+    k = topk_ids.shape[1]
+    tw = _contig(topk_weights.to(torch.float32))
+    ti = _contig(topk_ids.to(torch.int32))
+    out = torch.empty((T, H) if sum_topk else (T * k, H), dtype=x.dtype, device=x.device)
+    nws = int(lib.tsm_fused_moe_f32_workspace_size(T, H, I, E, k))
+    ws = torch.empty(max(nws, 1), dtype=torch.uint8, device=x.device)
+    check(lib.tsm_fused_moe_f32(ptr(x), ptr(w13), ptr(w2), ptr(tw), ptr(ti), T, H, I, E, k,
+                                int(sum_topk), ptr(out), ptr(ws), nws, stream_of(x)),
+          "fused_moe (fp32)")
+    return out
+
+
 def _fused_moe_impl(x, w13, w2, topk_weights, topk_ids, sum_topk, packed):
     _on_gpu(x, w13, w2, topk_weights, topk_ids)
     x, w13, w2 = _contig(x), _contig(w13), _contig(w2)
+    if not packed and x.dtype == torch.float32 and w13.dtype == torch.float32 \
+            and w2.dtype == torch.float32:
+        return _fused_moe_f32(x, w13, w2, topk_weights, topk_ids, sum_topk)
     if not packed:
         T, H, E, I = _check_weights(x, w13, w2)
         if _needs_padding(H, I):
@@ -315,6 +338,10 @@ def _moe_forward_impl(x, gate_w, w13, w2, top_k, renormalize, expert_map, bias, 
                       sum_topk, packed):
     _on_gpu(x, gate_w, w13, w2, expert_map, bias)
     x, gate_w, w13, w2 = _contig(x), _contig(gate_w), _contig(w13), _contig(w2)
+    if not packed and x.dtype == torch.float32:
+        # fp32 layer: the fused router (fp32 inputs) then the fp32 experts
+        w, ids, _ = moe_router(x, gate_w, top_k, renormalize, expert_map, bias, logits_bf16)
+        return _fused_moe_impl(x, w13, w2, w, ids, sum_topk, False)
     if packed:
         T, H, Hp, E, Ip = _check_packed(x, w13, w2)
         ragged = Hp != H
