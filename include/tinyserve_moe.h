@@ -208,6 +208,58 @@ int tsm_add_rmsnorm(const void* x, int64_t T, int H, int top_k, void* residual, 
                     const void* weight, float eps, void* out, hipStream_t stream);
 
 /*
+ * ---- Attention side of the qwen3_moe decoder (the end-to-end driver's own kernels) ----
+ *
+ * KV cache: K pages [num_pages, page, Hkv, D] bf16 (the reference's layout); V pages stored
+ * transposed, [num_pages, Hkv, D, page] bf16 (so both MFMA operands of P.V read contiguous
+ * memory). A cache slot is page_index * page + offset.
+ *
+ * In place on q [T, H, D] and k [T, Hkv, D] (strided rows, unit stride within a head): optional
+ * per-head RMSNorm (q_weight / k_weight [D] bf16, both or neither; rounded to bf16), then
+ * rotate-half RoPE with cos / sin [T, D/2] fp32 (row stride cs_stride):
+ *   [x1, x2] -> [bf16(x1 cos - x2 sin), bf16(x2 cos + x1 sin)]
+ * With k_cache given, also writes the rotated k and v [T, Hkv, D] into the cache at
+ * slot_mapping[t] (int64; negative: not written).
+ * Replaces qk_norm_rope / _qk_norm_rope_kernel (tinykernels.py:107-275) and serve.py's
+ * index_copy_ of K/V into the page pool (serve.py:898-904). Requires D even, D <= 128.
+ */
+int tsm_qk_norm_rope(void* q, int64_t T, int H, int64_t q_tok_stride, int64_t q_head_stride,
+                     void* k, int Hkv, int64_t k_tok_stride, int64_t k_head_stride,
+                     const void* v, int64_t v_tok_stride, int64_t v_head_stride, int D,
+                     const float* cos, const float* sin, int64_t cs_stride,
+                     const void* q_weight, const void* k_weight, float eps, void* k_cache,
+                     void* v_cache, int page, const int64_t* slot_mapping, hipStream_t stream);
+
+/*
+ * Paged causal attention over packed requests: request b owns query rows
+ * [query_start_loc[b], query_start_loc[b+1]) of q [T, H, D] and a context of
+ * cu_seqlens_k[b+1] - cu_seqlens_k[b] tokens whose pages are block_table[b, :]; its queries are
+ * the last q_len positions of that context, each attending to keys at positions <= its own.
+ * GQA: query head h reads KV head h / (H / Hkv). out [T, H, D] bf16 (strided like q).
+ * Requests with one query token run in one launch (each workgroup's four wavefronts split the
+ * context), longer ones in a second (skipped when max_query_len <= 1); the grids depend on T,
+ * num_seqs and Hkv only, so a step can be captured in a HIP graph.
+ * Replaces paged_attention / _paged_attn_kernel (tinykernels.py:309-1028); results are those
+ * of torch_ref_attention (serve.py:639-688). Requires D in {64, 128}, H / Hkv dividing 16,
+ * page % 4 == 0, 16-byte aligned q rows.
+ */
+int tsm_paged_attention(const void* q, int64_t T, int H, int64_t q_tok_stride,
+                        int64_t q_head_stride, const void* k_cache, const void* v_cache,
+                        int page, int Hkv, int D, const int32_t* query_start_loc,
+                        const int32_t* cu_seqlens_k, const int32_t* block_table,
+                        int64_t bt_stride, int num_seqs, int max_query_len, float scale,
+                        void* out, int64_t o_tok_stride, int64_t o_head_stride,
+                        hipStream_t stream);
+
+/*
+ * Greedy token choice: out[r] = the index of the largest of logits[r, 0..V) (row stride ld,
+ * dtype TSM_F32 or TSM_BF16), the lowest index among equal values (torch.argmax's first
+ * maximal index; serve.py's greedy path, temperature 0).
+ */
+int tsm_greedy_argmax(const void* logits, int dtype, int64_t rows, int64_t ld, int V,
+                      int64_t* out, hipStream_t stream);
+
+/*
  * MFMA-tiled ("packed") expert weights. No counterpart in the reference, which streams w13/w2 in
  * their checkpoint layout (tinykernels.py:1707-1738); this is a one-time reordering (same size)
  * after which every 16x16x32 MFMA operand of a 16-row block is 1 KiB of contiguous memory:

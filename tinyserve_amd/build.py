@@ -10,7 +10,7 @@ ROOT = os.path.dirname(PKG_DIR)
 CSRC = os.path.join(PKG_DIR, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 LIB_PATH = os.path.join(PKG_DIR, "libtinyserve_moe.so")
-SOURCES = ["capi.hip", "moe_route.hip", "moe_align.hip", "moe_gemm.hip", "moe_stream.hip", "moe_pack.hip", "moe_tile.hip", "moe_expert.hip", "moe_norm.hip", "moe_f32.hip"]
+SOURCES = ["capi.hip", "moe_route.hip", "moe_align.hip", "moe_gemm.hip", "moe_stream.hip", "moe_pack.hip", "moe_tile.hip", "moe_expert.hip", "moe_norm.hip", "moe_f32.hip", "attn.hip"]
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [
