@@ -1,6 +1,10 @@
-"""The qwen3_moe workload driver (tinyserve_amd/e2e.py) on a small shape: decoding one token
-against the KV cache reproduces the last-position logits of a prefill over the longer prompt,
-and greedy generation is deterministic."""
+"""The qwen3_moe workload driver (tinyserve_amd/e2e.py) on a small shape, against the decoder
+oracle (oracle/decoder_oracle.py, a restatement of serve.py's torch forward): prefill logits,
+and greedy decoding teacher-forced through the oracle; plus determinism and graph replay.
+
+Tolerance: logits within 3e-2 of the largest |logit| (bf16 activations through two layers; the
+kernels and the oracle round at the same points but sum in different orders). A greedy token
+must equal the oracle's argmax unless the oracle's top two logits are closer than that."""
 import pytest
 import torch
 
@@ -14,27 +18,52 @@ def small_cfg():
                           num_experts_per_tok=2, moe_intermediate_size=512)
 
 
-def test_decode_matches_prefill_and_is_deterministic(dev):
+def reference_logits(model, ids):
+    from oracle.decoder_oracle import decoder_reference
+    sd = {n: t.detach().cpu() for n, t in model.state_dict().items()}
+    return decoder_reference(sd, model.cfg, ids.cpu())
+
+
+def test_prefill_and_decode_against_oracle(dev):
     from tinyserve_amd.e2e import build_model, generate
-    model = build_model(small_cfg(), seed=3)
+    model = build_model(small_cfg(), seed=3, router_logits="fp32")
     g = torch.Generator(device=dev).manual_seed(7)
-    B, P = 4, 33
-    ids = torch.randint(0, 1000, (B, P + 1), device=dev, generator=g)
-    cache = model.new_cache(B, P + 1)
-    model(ids[:, :P], cache, 0)
-    step = model(ids[:, P:], cache, P)[:, -1]
-    full = model(ids, model.new_cache(B, P + 1), 0)[:, -1]
-    scale = full.abs().max().item()
-    assert (step - full).abs().max().item() <= 2e-2 * scale + 1e-3
-    # the graph-captured fixed-length decode step against the cache-slice forward
-    cache2 = model.new_cache(B, P + 4)
-    model(ids[:, :P], cache2, 0)
-    pos = torch.full((1,), P, dtype=torch.long, device=dev)
-    step2 = model.decode_step(ids[:, P:], cache2, pos)
-    assert (step2 - full).abs().max().item() <= 2e-2 * scale + 1e-3
-    t1, _, _ = generate(model, ids[:, :P], 6, graph=True)
-    t2, _, _ = generate(model, ids[:, :P], 6, graph=True)
-    t3, _, _ = generate(model, ids[:, :P], 6, graph=False)
+    B, P, N = 4, 33, 6
+    prompts = torch.randint(0, 1000, (B, P), device=dev, generator=g)
+    toks, _, _ = generate(model, prompts, N, graph=True)
+    full = torch.cat([prompts, toks[:, :-1]], 1)
+    ref = reference_logits(model, full)                 # [B, P + N - 1, vocab]
+    steps = ref[:, P - 1:]                              # logits that chose each new token
+    scale = steps.abs().max().item()
+    top2 = steps.topk(2, dim=-1).values
+    clear = (top2[..., 0] - top2[..., 1]) > 3e-2 * scale
+    agree = toks.cpu() == steps.argmax(-1)
+    assert bool(agree[clear].all()), (toks.cpu(), steps.argmax(-1))
+    assert clear.float().mean().item() > 0.5
+    # prefill logits themselves (last prompt position) through the driver's forward
+    from tinyserve_amd.e2e import PagedBatch
+    batch = PagedBatch(B, P, 16, dev)
+    caches = model.new_caches(batch.num_pages, 16)
+    meta, pos, last = batch.prefill_meta([P] * B)
+    seq = torch.repeat_interleave(torch.arange(B, device=dev), P)
+    meta.slot_mapping = batch.slots(seq, pos)
+    logits = model(prompts.reshape(-1), pos, meta, caches, last).cpu()
+    err = (logits - ref[:, P - 1]).abs().max().item()
+    assert err <= 3e-2 * scale, (err, scale)
+
+
+def test_generation_is_deterministic_and_graph_matches_eager(dev):
+    from tinyserve_amd.e2e import build_model, generate
+    model = build_model(small_cfg(), seed=5)
+    g = torch.Generator(device=dev).manual_seed(9)
+    prompts = torch.randint(0, 1000, (3, 20), device=dev, generator=g)
+    t1, _, _ = generate(model, prompts, 6, graph=True)
+    t2, _, _ = generate(model, prompts, 6, graph=True)
+    t3, _, _ = generate(model, prompts, 6, graph=False)
     assert torch.equal(t1, t2)
     assert torch.equal(t1, t3)  # replayed graph and eager steps agree
-    assert t1.shape == (B, 6) and int(t1.min()) >= 0 and int(t1.max()) < 1000
+    # prefilling one sequence at a time runs (the MoE kernels pick plans by batch size, so
+    # bits may differ from the packed prefill; the oracle test covers the values)
+    t4, _, _ = generate(model, prompts, 6, graph=True, prefill_chunk=1)
+    assert t4.shape == t1.shape
+    assert t1.shape == (3, 6) and int(t1.min()) >= 0 and int(t1.max()) < 1000

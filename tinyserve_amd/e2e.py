@@ -1,21 +1,32 @@
 """Minimal qwen3_moe model driver: the end-to-end workload around the MoE op.
 
-A random-init Qwen3-MoE decoder (the architecture of serve.py's qwen3_moe path: pre-norm
-residual blocks, GQA attention with per-head q/k RMSNorm and rotary embeddings, a SparseMoE
-feed-forward in every layer, final norm and LM head, serve.py:1100-1258) run as batched greedy
-generation: all prompts prefilled in one pass, then one token per sequence per step against a
-contiguous KV cache. Attention, norms and projections are stock PyTorch (SDPA, hipBLASLt GEMMs);
-every MoE block is `tinyserve_amd.SparseMoE` on the HIP kernels. This is a workload driver for
-measuring the op inside a model, not a serving engine: no paged KV cache, scheduler, sampling or
-tokenizer (prompts are synthetic token ids).
+A random-init Qwen3-MoE decoder with the structure of serve.py's Model / DecoderLayer
+(serve.py:1100-1258): residual stream carried between layers and added inside the norms
+(add_rmsnorm, serve.py:1185-1193), GQA attention with per-head q/k RMSNorm and rotary embeddings
+over a paged KV cache (serve.py:816-906), a SparseMoE feed-forward in every layer, final norm and
+LM head. Everything but the dense projections runs on this build's HIP kernels:
+    embedding / qkv_proj / o_proj / lm_head   torch (hipBLASLt GEMMs)
+    input norm + residual add                 ops.rmsnorm / ops.moe_combine_add_rmsnorm
+    q/k norm + RoPE + K/V page write          attention.qk_norm_rope
+    paged causal attention                    attention.paged_attention
+    MoE block                                 SparseMoE (router + experts), per-slot rows
+    MoE k-sum + next residual add + norm      ops.moe_combine_add_rmsnorm (one launch)
+    greedy token                              attention.greedy_argmax
+Requests are packed back to back (serve.py's flattened batch, AttnMetadata serve.py:627-637);
+`generate` prefills the prompts and then decodes one token per sequence per step, each decode
+step replayed from one captured HIP graph. It is a workload driver for measuring the op inside a
+model, not a serving engine: no scheduler, sampling or tokenizer (prompts are synthetic ids).
 """
 import time
 from dataclasses import dataclass
+from types import SimpleNamespace
 
 import torch
 import torch.nn.functional as F
 from torch import nn
 
+from . import ops
+from .attention import PagedKVCache, greedy_argmax, paged_attention, qk_norm_rope
 from .moe import SparseMoE
 
 
@@ -36,105 +47,70 @@ class Qwen3MoeConfig:
     rope_theta: float = 1e6
 
 
-def rms_norm(x, weight, eps):
-    """RMSNorm in fp32, weight applied after casting back (as HF Qwen3RMSNorm)."""
-    xf = x.float()
-    xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
-    return weight * xf.to(x.dtype)
-
-
-def rotary(x, cos, sin):
-    """Rotate-half rotary embedding; x [..., S, D], cos/sin [S, D]."""
-    h = x.shape[-1] // 2
-    rot = torch.cat((-x[..., h:], x[..., :h]), dim=-1)
-    return x * cos + rot * sin
-
-
 class Attention(nn.Module):
     def __init__(self, cfg):
         super().__init__()
-        self.nh, self.nkv, self.d = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
-        H = cfg.hidden_size
-        self.qkv_proj = nn.Linear(H, (self.nh + 2 * self.nkv) * self.d, bias=False)
-        self.o_proj = nn.Linear(self.nh * self.d, H, bias=False)
-        self.q_norm = nn.Parameter(torch.ones(self.d))
-        self.k_norm = nn.Parameter(torch.ones(self.d))
+        self.H, self.Hkv, self.D = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+        self.qkv_sizes = [self.H * self.D, self.Hkv * self.D, self.Hkv * self.D]
+        self.qkv_proj = nn.Linear(cfg.hidden_size, sum(self.qkv_sizes), bias=False)
+        self.o_proj = nn.Linear(self.H * self.D, cfg.hidden_size, bias=False)
+        self.q_norm = nn.Parameter(torch.ones(self.D))
+        self.k_norm = nn.Parameter(torch.ones(self.D))
         self.eps = cfg.rms_norm_eps
 
-    def forward(self, x, cos, sin, cache_k, cache_v, start):
-        B, S, _ = x.shape
-        q, k, v = self.qkv_proj(x).split(
-            [self.nh * self.d, self.nkv * self.d, self.nkv * self.d], dim=-1)
-        q = rms_norm(q.view(B, S, self.nh, self.d), self.q_norm, self.eps).transpose(1, 2)
-        k = rms_norm(k.view(B, S, self.nkv, self.d), self.k_norm, self.eps).transpose(1, 2)
-        v = v.view(B, S, self.nkv, self.d).transpose(1, 2)
-        q, k = rotary(q, cos, sin), rotary(k, cos, sin)
-        cache_k[:, :, start:start + S] = k
-        cache_v[:, :, start:start + S] = v
-        kk, vv = cache_k[:, :, :start + S], cache_v[:, :, :start + S]
-        # prefill (start 0): causal within the prompt; decode (S = 1): the whole cache
-        o = F.scaled_dot_product_attention(q, kk, vv, is_causal=S > 1, enable_gqa=True)
-        return self.o_proj(o.transpose(1, 2).reshape(B, S, self.nh * self.d))
-
-    def decode(self, x, cos, sin, cache_k, cache_v, pos, mask):
-        """One token per sequence at position `pos` (a device tensor), attending over the whole
-        fixed-length cache under `mask`: shapes and addresses never change, so a step can be
-        captured once in a HIP graph and replayed."""
-        B = x.shape[0]
-        q, k, v = self.qkv_proj(x).split(
-            [self.nh * self.d, self.nkv * self.d, self.nkv * self.d], dim=-1)
-        q = rms_norm(q.view(B, 1, self.nh, self.d), self.q_norm, self.eps).transpose(1, 2)
-        k = rms_norm(k.view(B, 1, self.nkv, self.d), self.k_norm, self.eps).transpose(1, 2)
-        v = v.view(B, 1, self.nkv, self.d).transpose(1, 2)
-        q, k = rotary(q, cos, sin), rotary(k, cos, sin)
-        cache_k.index_copy_(2, pos, k)
-        cache_v.index_copy_(2, pos, v)
-        # query heads grouped per kv head (head h reads kv head h // (nh / nkv), as SDPA's
-        # enable_gqa does): two batched matmuls over the cache, no K/V expansion
-        qg = q.reshape(B, self.nkv, self.nh // self.nkv, self.d)
-        s = torch.matmul(qg, cache_k.transpose(-1, -2)).float() * (self.d ** -0.5)
-        s = s.masked_fill(~mask, float("-inf"))
-        o = torch.matmul(torch.softmax(s, dim=-1).to(x.dtype), cache_v)  # [B, nkv, G, d]
-        return self.o_proj(o.reshape(B, 1, self.nh * self.d))
+    def forward(self, x, cos, sin, cache: PagedKVCache, meta):
+        T = x.shape[0]
+        q, k, v = self.qkv_proj(x).split(self.qkv_sizes, dim=-1)
+        q, k, v = q.view(T, self.H, self.D), k.view(T, self.Hkv, self.D), v.view(T, self.Hkv, self.D)
+        qk_norm_rope(q, k, cos, sin, self.q_norm, self.k_norm, self.eps, v, cache,
+                     meta.slot_mapping)
+        o = paged_attention(q, cache, meta, self.D ** -0.5)
+        return self.o_proj(o.view(T, self.H * self.D))
 
 
 class DecoderLayer(nn.Module):
-    def __init__(self, cfg):
+    def __init__(self, cfg, router_logits="model"):
         super().__init__()
         self.input_norm = nn.Parameter(torch.ones(cfg.hidden_size))
         self.post_attn_norm = nn.Parameter(torch.ones(cfg.hidden_size))
         self.attn = Attention(cfg)
-        self.mlp = SparseMoE(cfg)
+        self.mlp = SparseMoE(cfg, router_logits=router_logits)
         self.eps = cfg.rms_norm_eps
 
-    def forward(self, x, cos, sin, cache_k, cache_v, start):
-        x = x + self.attn(rms_norm(x, self.input_norm, self.eps), cos, sin, cache_k, cache_v,
-                          start)
-        B, S, H = x.shape
-        h = rms_norm(x, self.post_attn_norm, self.eps).reshape(B * S, H)
-        return x + self.mlp(h).view(B, S, H)
-
-    def decode(self, x, cos, sin, cache_k, cache_v, pos, mask):
-        x = x + self.attn.decode(rms_norm(x, self.input_norm, self.eps), cos, sin, cache_k,
-                                 cache_v, pos, mask)
-        B, _, H = x.shape
-        return x + self.mlp(rms_norm(x, self.post_attn_norm, self.eps).reshape(B, H)).view(B, 1, H)
+    def forward(self, x, residual, cos, sin, cache, meta):
+        """(x, residual) -> (MoE per-slot rows, residual), the reference's layer convention
+        (serve.py:1177-1183) with the MoE output left unsummed: the next norm sums it.
+        x is the previous layer's rows [T*k, H] (or the embeddings, for the first layer, with
+        residual None)."""
+        if residual is None:
+            h = ops.rmsnorm(x, self.input_norm, self.eps)
+            residual = x
+        else:
+            h = ops.moe_combine_add_rmsnorm(x, self.mlp.top_k, residual, self.input_norm,
+                                            self.eps)
+        a = self.attn(h, cos, sin, cache, meta)
+        h = ops.rmsnorm(a, self.post_attn_norm, self.eps, residual)
+        return self.mlp.rows(h), residual
 
 
 class Qwen3MoeModel(nn.Module):
-    def __init__(self, cfg):
+    def __init__(self, cfg, max_position=4096, router_logits="model"):
         super().__init__()
         self.cfg = cfg
         self.embed = nn.Embedding(cfg.vocab_size, cfg.hidden_size)
-        self.layers = nn.ModuleList(DecoderLayer(cfg) for _ in range(cfg.num_hidden_layers))
+        self.layers = nn.ModuleList(DecoderLayer(cfg, router_logits)
+                                    for _ in range(cfg.num_hidden_layers))
         self.norm = nn.Parameter(torch.ones(cfg.hidden_size))
         self.lm_head = nn.Linear(cfg.hidden_size, cfg.vocab_size, bias=False)
-        inv = 1.0 / (cfg.rope_theta ** (torch.arange(0, cfg.head_dim, 2).float() / cfg.head_dim))
-        self.register_buffer("inv_freq", inv, persistent=False)
+        D = cfg.head_dim
+        inv = 1.0 / cfg.rope_theta ** (torch.arange(0, D, 2, dtype=torch.float64) / D)
+        freqs = torch.outer(torch.arange(max_position, dtype=torch.float64), inv)
+        self.register_buffer("cos", freqs.cos().float(), persistent=False)
+        self.register_buffer("sin", freqs.sin().float(), persistent=False)
 
     @torch.no_grad()
     def init_random(self, seed=0, std=0.02):
-        """Random-init weights (N(0, std) matrices, unit norms) in place."""
+        """Random-init weights (N(0, std) matrices, unit norms) in place, then pack the experts."""
         g = torch.Generator(device=self.norm.device).manual_seed(seed)
         for name, p in self.named_parameters():
             if p.dim() >= 2:
@@ -144,65 +120,101 @@ class Qwen3MoeModel(nn.Module):
         for layer in self.layers:
             layer.mlp.pack()
 
-    def rope(self, start, S, device, dtype):
-        pos = torch.arange(start, start + S, device=device, dtype=torch.float32)
-        f = torch.outer(pos, self.inv_freq.to(device))
-        emb = torch.cat((f, f), dim=-1)
-        return emb.cos().to(dtype), emb.sin().to(dtype)
-
-    def new_cache(self, batch, max_len):
-        # zero-filled: masked positions take weight 0 in attention, and 0 * garbage could be NaN
+    def new_caches(self, num_pages, page=16):
         c = self.cfg
-        shape = (batch, c.num_key_value_heads, max_len, c.head_dim)
-        dev, dt = self.norm.device, self.norm.dtype
-        return [(torch.zeros(shape, device=dev, dtype=dt), torch.zeros(shape, device=dev, dtype=dt))
+        return [PagedKVCache.allocate(num_pages, page, c.num_key_value_heads, c.head_dim,
+                                      self.norm.device, self.norm.dtype)
                 for _ in range(c.num_hidden_layers)]
 
     @torch.no_grad()
-    def forward(self, ids, cache, start, last_only=True):
+    def forward(self, ids, positions, meta, caches, last_rows):
+        """ids / positions [T] (packed requests), meta as serve.AttnMetadata, last_rows [B]:
+        the packed row of each request's last token. Returns logits [B, vocab] (fp32)."""
         x = self.embed(ids)
-        cos, sin = self.rope(start, ids.shape[1], x.device, x.dtype)
-        for layer, (ck, cv) in zip(self.layers, cache):
-            x = layer(x, cos, sin, ck, cv, start)
-        if last_only:
-            x = x[:, -1:]
-        return self.lm_head(rms_norm(x, self.norm, self.cfg.rms_norm_eps)).float()
+        cos, sin = self.cos[positions], self.sin[positions]
+        residual = None
+        for layer, cache in zip(self.layers, caches):
+            x, residual = layer(x, residual, cos, sin, cache, meta)
+        h = ops.moe_combine_add_rmsnorm(x, self.cfg.num_experts_per_tok, residual, self.norm,
+                                        self.cfg.rms_norm_eps)
+        return self.lm_head(h[last_rows]).float()
 
-    @torch.no_grad()
-    def decode_step(self, tok, cache, pos):
-        """tok [B, 1] at position pos (int64 device tensor [1]) -> logits [B, vocab] fp32."""
-        x = self.embed(tok)
-        f = pos.float()[:, None] * self.inv_freq[None, :]
-        emb = torch.cat((f, f), dim=-1)
-        cos, sin = emb.cos().to(x.dtype), emb.sin().to(x.dtype)
-        L = cache[0][0].shape[2]
-        mask = (torch.arange(L, device=x.device) <= pos)[None, None, None, :]  # [1,1,1,L]
-        for layer, (ck, cv) in zip(self.layers, cache):
-            x = layer.decode(x, cos, sin, ck, cv, pos, mask)
-        return self.lm_head(rms_norm(x[:, 0], self.norm, self.cfg.rms_norm_eps)).float()
+
+class PagedBatch:
+    """Page assignment and device metadata for B sequences of up to max_len tokens: sequence b
+    owns pages 1 + b * pps .. (page 0 is the null page), so its block table row is fixed."""
+
+    def __init__(self, B, max_len, page, device):
+        self.B, self.page = B, page
+        self.pps = -(-max_len // page)
+        self.num_pages = 1 + B * self.pps
+        self.block_table = (1 + torch.arange(B * self.pps, dtype=torch.int32, device=device)
+                            ).view(B, self.pps)
+        self.device = device
+
+    def slots(self, seq, pos):
+        """Cache slot of token position `pos` of sequence `seq` (device tensors)."""
+        pg = self.block_table[seq, torch.div(pos, self.page, rounding_mode="floor")].long()
+        return pg * self.page + pos % self.page
+
+    def prefill_meta(self, lens):
+        """Metadata for prompts of lengths `lens` (list) packed back to back, from position 0."""
+        dev = self.device
+        qsl = [0]
+        for n in lens:
+            qsl.append(qsl[-1] + n)
+        seq = torch.repeat_interleave(torch.arange(len(lens), device=dev),
+                                      torch.tensor(lens, device=dev))
+        pos = torch.cat([torch.arange(n, device=dev) for n in lens])
+        starts = torch.tensor(qsl, dtype=torch.int32, device=dev)
+        meta = SimpleNamespace(query_start_loc=starts, cu_seqlens_k=starts.clone(),
+                               block_table=self.block_table[:len(lens)],
+                               num_seqs=len(lens), max_query_len=max(lens),
+                               slot_mapping=self.slots(seq, pos))
+        return meta, pos, starts[1:].long() - 1
 
 
 @torch.no_grad()
-def generate(model, prompts, new_tokens, graph=True):
+def generate(model, prompts, new_tokens, graph=True, page=16, prefill_chunk=None):
     """Greedy generation for a batch of equal-length prompts [B, P]. Returns (tokens [B, N],
-    prefill seconds, decode seconds). The prompts are prefilled in one pass; each decode step
-    runs on the fixed-length cache, captured once as a HIP graph and replayed (graph=True), as
-    serve.py replays captured decode steps, or eagerly."""
+    prefill seconds, decode seconds). Prompts are prefilled packed, `prefill_chunk` sequences at a
+    time (all by default); each decode step (one token per sequence) is captured once as a HIP
+    graph and replayed (graph=True), as serve.py replays captured decode steps, or run eagerly."""
     B, P = prompts.shape
-    cache = model.new_cache(B, P + new_tokens)
-    out = torch.empty(B, new_tokens, dtype=torch.long, device=prompts.device)
+    dev = prompts.device
+    batch = PagedBatch(B, P + new_tokens, page, dev)
+    caches = model.new_caches(batch.num_pages, page)
+    out = torch.empty(B, new_tokens, dtype=torch.long, device=dev)
+    chunk = prefill_chunk or B
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    out[:, 0] = model(prompts, cache, 0)[:, -1].argmax(-1)
+    for b0 in range(0, B, chunk):
+        nb = min(chunk, B - b0)
+        meta, pos, last = batch.prefill_meta([P] * nb)
+        meta.block_table = batch.block_table[b0:b0 + nb]
+        seq = torch.repeat_interleave(torch.arange(b0, b0 + nb, device=dev), P)
+        meta.slot_mapping = batch.slots(seq, pos)
+        logits = model(prompts[b0:b0 + nb].reshape(-1), pos, meta, caches, last)
+        out[b0:b0 + nb, 0] = greedy_argmax(logits)
     torch.cuda.synchronize()
     t1 = time.perf_counter()
-    tok = out[:, :1].clone()
-    pos = torch.full((1,), P, dtype=torch.long, device=prompts.device)
-    col = torch.ones(1, dtype=torch.long, device=prompts.device)
+
+    # decode state, all on the device: the step reads and advances it, so it can be replayed
+    tok = out[:, 0].clone()
+    pos = torch.full((B,), P, dtype=torch.long, device=dev)
+    col = torch.ones(1, dtype=torch.long, device=dev)
+    seqs = torch.arange(B, device=dev)
+    meta = SimpleNamespace(query_start_loc=torch.arange(B + 1, dtype=torch.int32, device=dev),
+                           cu_seqlens_k=torch.zeros(B + 1, dtype=torch.int32, device=dev),
+                           block_table=batch.block_table, num_seqs=B, max_query_len=1,
+                           slot_mapping=torch.zeros(B, dtype=torch.long, device=dev))
+    rows = torch.arange(B, device=dev)
 
     def step():
-        nxt = model.decode_step(tok, cache, pos).argmax(-1, keepdim=True)
-        out.index_copy_(1, col, nxt)
+        meta.cu_seqlens_k[1:].copy_(torch.cumsum(pos + 1, 0))
+        meta.slot_mapping.copy_(batch.slots(seqs, pos))
+        nxt = greedy_argmax(model(tok, pos, meta, caches, rows))
+        out.index_copy_(1, col, nxt[:, None])
         tok.copy_(nxt)
         pos.add_(1)
         col.add_(1)
@@ -219,7 +231,7 @@ def generate(model, prompts, new_tokens, graph=True):
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
             step()
-        tok.copy_(out[:, :1])
+        tok.copy_(out[:, 0])
         pos.fill_(P)
         col.fill_(1)
         torch.cuda.synchronize()
@@ -234,12 +246,12 @@ def generate(model, prompts, new_tokens, graph=True):
     return out, t1 - t0, t2 - t1
 
 
-def build_model(cfg=None, device="cuda", seed=0):
+def build_model(cfg=None, device="cuda", seed=0, router_logits="model", max_position=4096):
     cfg = cfg or Qwen3MoeConfig()
     torch.set_default_dtype(torch.bfloat16)
     try:
         with torch.device(device):
-            model = Qwen3MoeModel(cfg)
+            model = Qwen3MoeModel(cfg, max_position, router_logits)
     finally:
         torch.set_default_dtype(torch.float32)
     model.init_random(seed)

@@ -178,22 +178,29 @@ class SparseMoE(nn.Module):
     def _logits_bf16(self):
         return self.router_logits == "model" and self.gate.weight.dtype == torch.bfloat16
 
-    def forward(self, x):
+    def rows(self, x):
+        """The block's per-slot rows [T * top_k, H] (row t*k + s = routing weight x expert output
+        of token t's slot s), unsummed: the reference's fused_moe(..., sum_topk=False)
+        (serve.py:1084-1085), for a caller that fuses the k-sum into what follows
+        (ops.moe_combine_add_rmsnorm)."""
+        return self.forward(x, sum_topk=False)
+
+    def forward(self, x, sum_topk: bool = True):
         # the packed layout is for the bf16 matrix-core kernels; fp32 layers run unpacked
         if self.packed and (self.weights_packed or self.w13.dtype == torch.bfloat16):
             w13, w2 = self.pack()
             if self.router == "fused":
                 return ops.moe_forward_packed(x, self.gate.weight, w13, w2, self.top_k,
                                               self.norm_topk_prob, self.expert_map, None,
-                                              self._logits_bf16())
+                                              self._logits_bf16(), sum_topk)
             topk_weights, topk_ids = ops.moe_route(self.gate(x), self.top_k,
                                                    self.norm_topk_prob, self.expert_map)
-            return ops.fused_moe_packed(x, w13, w2, topk_weights, topk_ids)
+            return ops.fused_moe_packed(x, w13, w2, topk_weights, topk_ids, sum_topk)
         self.unpack()
         if self.router == "fused":
             return ops.moe_forward(x, self.gate.weight, self.w13, self.w2, self.top_k,
                                    self.norm_topk_prob, self.expert_map, None,
-                                   self._logits_bf16())
+                                   self._logits_bf16(), sum_topk)
         topk_weights, topk_ids = ops.moe_route(self.gate(x), self.top_k, self.norm_topk_prob,
                                                self.expert_map)
-        return ops.fused_moe(x, self.w13, self.w2, topk_weights, topk_ids)
+        return ops.fused_moe(x, self.w13, self.w2, topk_weights, topk_ids, sum_topk)
