@@ -218,8 +218,8 @@ int tsm_add_rmsnorm(const void* x, int64_t T, int H, int top_k, void* residual, 
  * per-head RMSNorm (q_weight / k_weight [D] bf16, both or neither; rounded to bf16), then
  * rotate-half RoPE with cos / sin [T, D/2] fp32 (row stride cs_stride):
  *   [x1, x2] -> [bf16(x1 cos - x2 sin), bf16(x2 cos + x1 sin)]
- * With k_cache given, also writes the rotated k and v [T, Hkv, D] into the cache at
- * slot_mapping[t] (int64; negative: not written).
+ * With k_cache given, also writes the rotated k and v [T, Hkv, D] into the cache (num_pages
+ * pages of `page` slots) at slot_mapping[t] (int64; negative or past the pool: not written).
  * Replaces qk_norm_rope / _qk_norm_rope_kernel (tinykernels.py:107-275) and serve.py's
  * index_copy_ of K/V into the page pool (serve.py:898-904). Requires D even, D <= 128.
  */
@@ -228,7 +228,8 @@ int tsm_qk_norm_rope(void* q, int64_t T, int H, int64_t q_tok_stride, int64_t q_
                      const void* v, int64_t v_tok_stride, int64_t v_head_stride, int D,
                      const float* cos, const float* sin, int64_t cs_stride,
                      const void* q_weight, const void* k_weight, float eps, void* k_cache,
-                     void* v_cache, int page, const int64_t* slot_mapping, hipStream_t stream);
+                     void* v_cache, int64_t num_pages, int page, const int64_t* slot_mapping,
+                     hipStream_t stream);
 
 /*
  * Paged causal attention over packed requests: request b owns query rows
@@ -236,6 +237,8 @@ int tsm_qk_norm_rope(void* q, int64_t T, int H, int64_t q_tok_stride, int64_t q_
  * cu_seqlens_k[b+1] - cu_seqlens_k[b] tokens whose pages are block_table[b, :]; its queries are
  * the last q_len positions of that context, each attending to keys at positions <= its own.
  * GQA: query head h reads KV head h / (H / Hkv). out [T, H, D] bf16 (strided like q).
+ * Block-table entries are clamped into [0, num_pages) (metadata is trusted, as in the
+ * reference, but a wrong entry cannot address memory outside the caches).
  * Requests with one query token run in one launch (each workgroup's four wavefronts split the
  * context), longer ones in a second (skipped when max_query_len <= 1); the grids depend on T,
  * num_seqs and Hkv only, so a step can be captured in a HIP graph.
@@ -245,7 +248,7 @@ int tsm_qk_norm_rope(void* q, int64_t T, int H, int64_t q_tok_stride, int64_t q_
  */
 int tsm_paged_attention(const void* q, int64_t T, int H, int64_t q_tok_stride,
                         int64_t q_head_stride, const void* k_cache, const void* v_cache,
-                        int page, int Hkv, int D, const int32_t* query_start_loc,
+                        int64_t num_pages, int page, int Hkv, int D, const int32_t* query_start_loc,
                         const int32_t* cu_seqlens_k, const int32_t* block_table,
                         int64_t bt_stride, int num_seqs, int max_query_len, float scale,
                         void* out, int64_t o_tok_stride, int64_t o_head_stride,

@@ -51,9 +51,9 @@ def _load():
                                     P, P, SZ, P], I32),
         "tsm_moe_combine": ([P, I64, I32, I32, P, P], I32),
         "tsm_qk_norm_rope": ([P, I64, I32, I64, I64, P, I32, I64, I64, P, I64, I64, I32, P, P, I64,
-                              P, P, ctypes.c_float, P, P, I32, P, P], I32),
-        "tsm_paged_attention": ([P, I64, I32, I64, I64, P, P, I32, I32, I32, P, P, P, I64, I32,
-                                 I32, ctypes.c_float, P, I64, I64, P], I32),
+                              P, P, ctypes.c_float, P, P, I64, I32, P, P], I32),
+        "tsm_paged_attention": ([P, I64, I32, I64, I64, P, P, I64, I32, I32, I32, P, P, P, I64,
+                                 I32, I32, ctypes.c_float, P, I64, I64, P], I32),
         "tsm_greedy_argmax": ([P, I32, I64, I64, I32, P, P], I32),
         "tsm_add_rmsnorm": ([P, I64, I32, I32, P, I32, P, ctypes.c_float, P, P], I32),
         "tsm_moe_forward_workspace_size": ([I64, I32, I32, I32, I32], SZ),

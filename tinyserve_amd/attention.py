@@ -63,19 +63,19 @@ def qk_norm_rope(q: Tensor, k: Tensor, cos: Tensor, sin: Tensor,
     if (q_weight is None) != (k_weight is None):
         raise ValueError("q and k norm weights come together")
     kc = vc = None
-    page = 0
+    page = num_pages = 0
     if cache is not None:
         if v is None or slot_mapping is None:
             raise ValueError("a cache write needs v and slot_mapping")
         if v.stride(-1) != 1:
             raise ValueError("v heads must be contiguous in the last dimension")
-        kc, vc, page = cache.k, cache.v, cache.page
+        kc, vc, page, num_pages = cache.k, cache.v, cache.page, cache.k.shape[0]
         slot_mapping = slot_mapping.to(torch.int64).contiguous()
     check(lib.tsm_qk_norm_rope(
         ptr(q), T, H, q.stride(0), q.stride(1), ptr(k), Hkv, k.stride(0), k.stride(1),
         ptr(v), v.stride(0) if v is not None else 0, v.stride(1) if v is not None else 0, D,
         ptr(cos), ptr(sin), cos.stride(0), ptr(q_weight), ptr(k_weight), float(eps), ptr(kc),
-        ptr(vc), page, ptr(slot_mapping), stream_of(q)), "qk_norm_rope")
+        ptr(vc), num_pages, page, ptr(slot_mapping), stream_of(q)), "qk_norm_rope")
     return q, k
 
 
@@ -95,7 +95,8 @@ def paged_attention(q: Tensor, cache: PagedKVCache, meta, scale: float) -> Tenso
     if bt.dtype != torch.int32 or bt.stride(-1) != 1:
         bt = bt.to(torch.int32).contiguous()
     check(lib.tsm_paged_attention(
-        ptr(q), T, H, q.stride(0), q.stride(1), ptr(cache.k), ptr(cache.v), cache.page, Hkv, D,
+        ptr(q), T, H, q.stride(0), q.stride(1), ptr(cache.k), ptr(cache.v), cache.k.shape[0],
+        cache.page, Hkv, D,
         ptr(qsl), ptr(cuk), ptr(bt), bt.stride(0), int(meta.num_seqs), int(meta.max_query_len),
         float(scale), ptr(out), out.stride(0), out.stride(1), stream_of(q)), "paged_attention")
     return out

@@ -33,6 +33,7 @@ struct QkArgs {
     bf16_t* k_cache;   // [num_pages, page, Hkv, D] or null (no cache write)
     bf16_t* v_cache;   // [num_pages, Hkv, D, page]
     int page;
+    int64_t num_slots;     // num_pages * page: slots at or past it are not written
     const int64_t* slots;  // [T] cache slot (page * page_size + offset); < 0: not written
 };
 
@@ -45,7 +46,8 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(QkArgs p) {
     const bool on = lane < half;
     const float c = on ? p.cos[(int64_t)t * p.cs + lane] : 0.0f;
     const float s = on ? p.sin[(int64_t)t * p.cs + lane] : 0.0f;
-    const int64_t slot = p.k_cache ? p.slots[t] : -1;
+    int64_t slot = p.k_cache ? p.slots[t] : -1;
+    if (slot >= p.num_slots) slot = -1;
     const int n_rot = p.H + p.Hkv;
     for (int hh = wave; hh < n_rot + (slot >= 0 ? p.Hkv : 0); hh += 4) {
         if (hh >= n_rot) {  // V rows go to the transposed V pages unchanged
@@ -98,8 +100,18 @@ struct AttnArgs {
     const int32_t* bt;     // [B, bt_stride] block table
     int64_t bt_stride;
     int B, Hkv, page;
+    int64_t T;             // query rows: requests reaching past them are skipped
+    int64_t num_pages;     // page indices are clamped into [0, num_pages)
     float scale_log2;      // softmax scale * log2(e)
 };
+
+// Page of context position `pos` (< kv_len): the block-table entry, clamped into the pool, so
+// that inconsistent metadata reads a wrong page rather than memory outside the caches.
+__device__ __forceinline__ int64_t page_of(const int32_t* bt_row, int pos, const AttnArgs& p) {
+    const int64_t col = min((int64_t)(pos / p.page), p.bt_stride - 1);
+    const int64_t pg = bt_row[col];
+    return pg < 0 ? 0 : (pg >= p.num_pages ? p.num_pages - 1 : pg);
+}
 
 constexpr int kAttnWaves = 4;
 
@@ -157,6 +169,8 @@ __global__ __launch_bounds__(kAttnWaves * 64) void paged_attn_kernel(AttnArgs p)
     const int q_len = p.qsl[b + 1] - q_start;
     const int kv_len = p.cu_k[b + 1] - p.cu_k[b];
     if (DECODE ? q_len != 1 : (q_len < 2 || tile * TQ >= q_len)) return;
+    // inconsistent metadata (queries outside q, a context shorter than its queries): skipped
+    if (q_start < 0 || q_start + q_len > p.T || kv_len < q_len) return;
 
     const int tok0 = DECODE ? 0 : tile * TQ + wave * TPW;   // this wavefront's first token
     const int tok_r = tok0 + r / GROUP;
@@ -198,7 +212,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void paged_attn_kernel(AttnArgs p)
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
             const int kc = min(key0 + 16 * t + r, kv_len - 1);
-            const int64_t pg = bt_row[kc / p.page];
+            const int64_t pg = page_of(bt_row, kc, p);
             const bf16_t* src = p.k_cache + (pg * p.page + kc % p.page) * kc_tok + kvh * D + 8 * qd;
 #pragma unroll
             for (int s = 0; s < NDS; ++s) kop[t][s] = *reinterpret_cast<const u32x4*>(src + 32 * s);
@@ -209,7 +223,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void paged_attn_kernel(AttnArgs p)
         for (int h = 0; h < 2; ++h) {
             const int g = key0 + 16 * h + 4 * qd;
             const int ga = g < kv_len ? g : ((kv_len - 1) & ~3);
-            const int64_t pg = bt_row[ga / p.page];
+            const int64_t pg = page_of(bt_row, ga, p);
             const bf16_t* src =
                 p.v_cache + ((pg * p.Hkv + kvh) * D + r) * p.page + ga % p.page;
 #pragma unroll
@@ -393,8 +407,8 @@ extern "C" int tsm_qk_norm_rope(void* q, int64_t T, int H, int64_t q_tok_stride,
                                 int64_t k_head_stride, const void* v, int64_t v_tok_stride,
                                 int64_t v_head_stride, int D, const float* cos, const float* sin,
                                 int64_t cs_stride, const void* q_weight, const void* k_weight,
-                                float eps, void* k_cache, void* v_cache, int page,
-                                const int64_t* slot_mapping, hipStream_t stream) {
+                                float eps, void* k_cache, void* v_cache, int64_t num_pages,
+                                int page, const int64_t* slot_mapping, hipStream_t stream) {
     clear_error();
     TSM_REQUIRE(T >= 0 && T <= 0x7fffffffll && H >= 1 && Hkv >= 1 && H % Hkv == 0, TSM_E_ARG,
                 "bad sizes (T=%lld H=%d Hkv=%d)", (long long)T, H, Hkv);
@@ -402,8 +416,9 @@ extern "C" int tsm_qk_norm_rope(void* q, int64_t T, int H, int64_t q_tok_stride,
                 "head_dim must be even and <= 128 (got %d)", D);
     TSM_REQUIRE((q_weight == nullptr) == (k_weight == nullptr), TSM_E_ARG,
                 "q and k norm weights come together");
-    TSM_REQUIRE(!k_cache || (v_cache && v && slot_mapping && page >= 1), TSM_E_ARG,
-                "a cache write needs v, both caches, slot_mapping and page >= 1");
+    TSM_REQUIRE(!k_cache || (v_cache && v && slot_mapping && page >= 1 && num_pages >= 1),
+                TSM_E_ARG, "a cache write needs v, both caches, slot_mapping, page >= 1 and "
+                "num_pages >= 1");
     if (T == 0) return TSM_OK;
     TSM_REQUIRE(q && k && cos && sin, TSM_E_ARG, "null pointer argument");
     QkArgs a{};
@@ -429,6 +444,7 @@ extern "C" int tsm_qk_norm_rope(void* q, int64_t T, int H, int64_t q_tok_stride,
     a.k_cache = (bf16_t*)k_cache;
     a.v_cache = (bf16_t*)v_cache;
     a.page = page;
+    a.num_slots = k_cache ? num_pages * page : 0;
     a.slots = slot_mapping;
     hipLaunchKernelGGL(qk_norm_rope_kernel, dim3((unsigned)T), dim3(256), 0, stream, a);
     return check_launch("qk_norm_rope_kernel");
@@ -436,7 +452,8 @@ extern "C" int tsm_qk_norm_rope(void* q, int64_t T, int H, int64_t q_tok_stride,
 
 extern "C" int tsm_paged_attention(const void* q, int64_t T, int H, int64_t q_tok_stride,
                                    int64_t q_head_stride, const void* k_cache,
-                                   const void* v_cache, int page, int Hkv, int D,
+                                   const void* v_cache, int64_t num_pages, int page, int Hkv,
+                                   int D,
                                    const int32_t* query_start_loc, const int32_t* cu_seqlens_k,
                                    const int32_t* block_table, int64_t bt_stride, int num_seqs,
                                    int max_query_len, float scale, void* out,
@@ -452,6 +469,8 @@ extern "C" int tsm_paged_attention(const void* q, int64_t T, int H, int64_t q_to
                 "query heads per KV head must divide 16 (got %d)", group);
     TSM_REQUIRE(D == 64 || D == 128, TSM_E_SHAPE, "head_dim must be 64 or 128 (got %d)", D);
     TSM_REQUIRE(page >= 4 && page % 4 == 0, TSM_E_SHAPE, "page size must be a multiple of 4");
+    TSM_REQUIRE(num_pages >= 1 && bt_stride >= 1, TSM_E_ARG,
+                "num_pages and the block-table row stride must be >= 1");
     TSM_REQUIRE(q_head_stride % 8 == 0 && q_tok_stride % 8 == 0 && o_head_stride % 4 == 0 &&
                     o_tok_stride % 4 == 0,
                 TSM_E_ARG, "q rows must be 16-byte and out rows 8-byte aligned");
@@ -474,6 +493,8 @@ extern "C" int tsm_paged_attention(const void* q, int64_t T, int H, int64_t q_to
     a.B = num_seqs;
     a.Hkv = Hkv;
     a.page = page;
+    a.num_pages = num_pages;
+    a.T = T;
     a.scale_log2 = scale * 1.4426950408889634f;
     const bool ok = D == 128 ? launch_attn_d<128>(a, group, T, max_query_len, stream)
                              : launch_attn_d<64>(a, group, T, max_query_len, stream);
