@@ -113,6 +113,18 @@ int tsm_silu_and_mul(const void* gate, int64_t gate_stride, const void* up, int6
 int tsm_moe_block_m(int64_t T, int H, int I, int E, int top_k, int weight_layout);
 
 /*
+ * Install a tile height for the plans of fused_moe / moe_forward with the given weight layout,
+ * for assignment counts numel = T * top_k in the power-of-two buckets that [numel_lo, numel_hi]
+ * touches (bucket b: 2^b <= numel < 2^(b+1)); block_m = -1 restores the static table there.
+ * 0 selects the expert-major stages (used only where their size limits allow), 16 / 64 (and 128
+ * with packed weights) the tiled stages. Process-wide; plans already captured in a HIP graph keep
+ * their kernels. Workspace sizes follow the installed heights, so query them after installing.
+ * The build's counterpart of the autotuning of autotune_fused_moe (tinykernels.py:1798-1811):
+ * kernels.autotune_fused_moe times the candidates and installs the fastest.
+ */
+int tsm_moe_set_block_m(int64_t numel_lo, int64_t numel_hi, int weight_layout, int block_m);
+
+/*
  * Experts on sorted rows: align + grouped gate_up GEMM with the SwiGLU epilogue + grouped down GEMM
  * scaled by the routing weight + (sum_topk) the deterministic fixed-order k-sum.
  * Replaces fused_moe (tinykernels.py:1767-1796) with _moe_gemm/_fused_moe_kernel

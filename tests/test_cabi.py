@@ -100,3 +100,27 @@ def test_padded_shape_and_norm_validation(lib):
     assert b"residual" in lib.tsm_last_error()
     assert nf(None, 4, 2048, 8, None, 0, P(256), 1e-6, P(512), None) == -1      # null x
     assert nf(None, 0, 2048, 8, None, 0, None, 1e-6, None, None) == 0           # empty batch
+
+
+def test_plan_overrides(lib):
+    """Installed tile heights change the plan (and the workspace follows); -1 restores it."""
+    I32, I64 = ctypes.c_int, ctypes.c_int64
+    lib.tsm_moe_set_block_m.argtypes = [I64, I64, I32, I32]
+    lib.tsm_moe_block_m.argtypes = [I64, I32, I32, I32, I32, I32]
+    ws = lib.tsm_fused_moe_workspace_size
+    ws.restype = ctypes.c_size_t
+    ws.argtypes = [I64, I32, I32, I32, I32]
+    base = lib.tsm_moe_block_m(64, 2048, 768, 128, 8, 0)
+    assert base == 0                                        # expert-major at T=64
+    w0 = ws(64, 2048, 768, 128, 8)
+    assert lib.tsm_moe_set_block_m(512, 512, 0, 64) == 0
+    assert lib.tsm_moe_block_m(64, 2048, 768, 128, 8, 0) == 64
+    assert lib.tsm_moe_block_m(64, 2048, 768, 128, 8, 1) == 0   # the other layout untouched
+    assert ws(64, 2048, 768, 128, 8) > w0                   # padded rows for 64-row tiles
+    assert lib.tsm_moe_set_block_m(512, 512, 0, 128) == -2  # no 128-row reference kernel
+    assert lib.tsm_moe_set_block_m(512, 512, 1, 128) == 0
+    assert lib.tsm_moe_block_m(64, 2048, 768, 128, 8, 1) == 128
+    assert lib.tsm_moe_set_block_m(1, 1 << 40, 0, -1) == 0
+    assert lib.tsm_moe_set_block_m(1, 1 << 40, 1, -1) == 0
+    assert lib.tsm_moe_block_m(64, 2048, 768, 128, 8, 0) == base
+    assert lib.tsm_moe_set_block_m(0, 4, 0, 16) == -1       # numel_lo >= 1

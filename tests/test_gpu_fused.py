@@ -436,3 +436,24 @@ def test_tiny_config_fp32(dev, tsm, T):
         m.w13.copy_(w13)
         m.w2.copy_(w2)
         assert torch.equal(m(x), out)
+
+
+def test_autotune_installs_plans(dev, tsm, qwen_layer):
+    """autotune_fused_moe times the candidate tile heights per batch-size bucket and installs
+    the fastest; the plans it installs keep parity with the oracle, and clearing them restores
+    the static table."""
+    from tinyserve_amd import kernels
+    (gw, w13, w2), (_, w13c, w2c) = qwen_layer
+    before = {T: kernels.moe_block_m(T, 2048, 768, 128, 8) for T in (1, 64, 512)}
+    table = kernels.autotune_fused_moe(w13, w2, 8, 512)
+    assert set(table) == {1 << (n.bit_length() - 1) for n in (8, 16, 32, 64, 128, 256, 512,
+                                                                 1024, 2048, 4096)}
+    for T in (1, 64, 512):
+        bm, _ = table[1 << ((T * 8).bit_length() - 1)]
+        assert kernels.moe_block_m(T, 2048, 768, 128, 8) == bm
+        x = xrand(T, 2048, dev, 900 + T)
+        w, ids, _ = tsm.moe_router(x, gw, 8, True)
+        ref = moe_reference(x.cpu(), w13c, w2c, w.cpu(), ids.cpu().long())
+        assert_close(tsm.fused_moe(x, w13, w2, w, ids), ref, f"autotuned T={T} bm={bm}")
+    kernels.set_moe_block_m(1, 1 << 30, -1)
+    assert {T: kernels.moe_block_m(T, 2048, 768, 128, 8) for T in (1, 64, 512)} == before

@@ -35,6 +35,7 @@ def _load():
         "tsm_moe_align": ([P, I64, I32, I32, P, P, P, P, SZ, P], I32),
         "tsm_silu_and_mul": ([P, I64, P, I64, P, I64, I64, I64, P], I32),
         "tsm_moe_block_m": ([I64, I32, I32, I32, I32, I32], I32),
+        "tsm_moe_set_block_m": ([I64, I64, I32, I32], I32),
         "tsm_fused_moe_workspace_size": ([I64, I32, I32, I32, I32], SZ),
         "tsm_fused_moe": ([P, P, P, P, P, I64, I32, I32, I32, I32, I32, P, P, SZ, P], I32),
         "tsm_fused_moe_f32_workspace_size": ([I64, I32, I32, I32, I32], SZ),

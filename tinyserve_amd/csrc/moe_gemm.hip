@@ -12,6 +12,8 @@
 // order so the down GEMM reads contiguous rows, and the k-sum is a fixed-order pass (slot 0..k-1)
 // rather than a reduction of unspecified order.
 #include <algorithm>
+#include <atomic>
+#include <mutex>
 #include "common.h"
 #include "internal.h"
 #include "tinyserve_moe.h"
@@ -257,8 +259,35 @@ struct Plan {
     int block_m;
 };
 
+bool block_m_supported(int block_m, bool packed);
+
+// Tile heights installed by autotuning (tsm_moe_set_block_m), per weight layout and per
+// power-of-two bucket of the assignment count (bucket b holds numel in [2^b, 2^(b+1))); -1 = the
+// static table. Read on every plan, written rarely: relaxed atomics.
+constexpr int kBuckets = 40;
+std::atomic<int> g_block_m_override[2][kBuckets];
+std::once_flag g_override_init;
+
+void init_overrides() {
+    for (auto& layout : g_block_m_override)
+        for (auto& b : layout) b.store(-1, std::memory_order_relaxed);
+}
+
+int numel_bucket(int64_t numel) {
+    int b = 0;
+    while (b + 1 < kBuckets && (int64_t(1) << (b + 1)) <= numel) ++b;
+    return b;
+}
+
 Plan plan_for(int64_t T, int H, int I, int E, int top_k, bool packed) {
     const int64_t numel = T * top_k;
+    std::call_once(g_override_init, init_overrides);
+    if (numel >= 1) {
+        const int o = g_block_m_override[packed][numel_bucket(numel)].load(std::memory_order_relaxed);
+        // an installed height applies where its kernels take the shape
+        if (o == 0 && expert_path_supported(numel, H, I, E)) return Plan{0};
+        if (o > 0 && block_m_supported(o, packed)) return Plan{o};
+    }
     if (numel >= 1 && numel <= 12ll * E && expert_path_supported(numel, H, I, E))
         return Plan{0};
     if (numel <= 4ll * E) return Plan{16};
@@ -470,6 +499,22 @@ int run_experts(const void* x, const void* w13, const void* w2, const float* top
 }  // namespace tsm
 
 using namespace tsm;
+
+extern "C" int tsm_moe_set_block_m(int64_t numel_lo, int64_t numel_hi, int weight_layout,
+                                   int block_m) {
+    clear_error();
+    TSM_REQUIRE(numel_lo >= 1 && numel_hi >= numel_lo, TSM_E_ARG,
+                "need 1 <= numel_lo <= numel_hi (got %lld, %lld)", (long long)numel_lo,
+                (long long)numel_hi);
+    TSM_REQUIRE(weight_layout == TSM_LAYOUT_REFERENCE || weight_layout == TSM_LAYOUT_PACKED,
+                TSM_E_ARG, "unknown weight layout %d", weight_layout);
+    TSM_REQUIRE(block_m == -1 || block_m == 0 || block_m_supported(block_m, weight_layout != 0),
+                TSM_E_SHAPE, "block_m %d has no kernel for this weight layout", block_m);
+    std::call_once(g_override_init, init_overrides);
+    for (int b = numel_bucket(numel_lo); b <= numel_bucket(numel_hi); ++b)
+        g_block_m_override[weight_layout != 0][b].store(block_m, std::memory_order_relaxed);
+    return TSM_OK;
+}
 
 extern "C" int tsm_moe_block_m(int64_t T, int H, int I, int E, int top_k, int weight_layout) {
     (void)H;

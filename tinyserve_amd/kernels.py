@@ -8,6 +8,10 @@ the gfx950 HIP kernels. `SparseMoE.forward` (serve.py:1076-1087) calls these thr
     silu_and_mul(gate, up)                                     tinykernels.py:299
     fused_moe(x, w13, w2, topk_weights, topk_ids, sum_topk)    tinykernels.py:1767
     autotune_fused_moe(w13, w2, top_k, max_num_tokens)         tinykernels.py:1799
+
+autotune_fused_moe times the kernel families and tile heights this build has (expert-major,
+16-, 64- and, with packed weights, 128-row tiles) per power-of-two bucket of assignment counts and
+installs the fastest in the library's plan table (set_moe_block_m).
 """
 import torch
 
@@ -45,13 +49,59 @@ def moe_block_m(T: int, H: int, I: int, E: int, top_k: int, packed: bool = False
     return int(lib.tsm_moe_block_m(T, H, I, E, top_k, int(packed)))
 
 
+def set_moe_block_m(numel_lo: int, numel_hi: int, block_m: int, packed: bool = False):
+    """Install a tile height for assignment counts in [numel_lo, numel_hi] (their power-of-two
+    buckets); block_m = -1 restores the static table (tsm_moe_set_block_m)."""
+    from ._lib import check
+    check(lib.tsm_moe_set_block_m(numel_lo, numel_hi, int(packed), block_m), "set_moe_block_m")
+
+
+def _candidates(numel: int, E: int, packed: bool):
+    c = [16, 64] + ([128] if packed else [])
+    if numel <= 4096:   # the expert-major stages' row limit
+        c.insert(0, 0)
+    return c
+
+
 @torch.inference_mode()
-def autotune_fused_moe(w13: torch.Tensor, w2: torch.Tensor, top_k: int, max_num_tokens: int):
-    """The kernel choice is a static table, so there is nothing to tune: this warms the code objects
-    up for the same two batch sizes the reference tunes at (1 and max_num_tokens)."""
+def autotune_fused_moe(w13: torch.Tensor, w2: torch.Tensor, top_k: int, max_num_tokens: int,
+                       packed: bool = False, reps: int = 5):
+    """Time the tile heights fused_moe can run for batch sizes 1, 2, 4, ... up to
+    max_num_tokens (random routing on the real expert weights, as the reference tunes,
+    tinykernels.py:1798-1811) and install the fastest for each power-of-two bucket of
+    assignment counts. `packed`: w13/w2 are pack_moe_weights output and the packed-layout plans
+    are tuned. Returns {numel bucket start: (block_m, microseconds)}."""
+    fn = ops.fused_moe_packed if packed else fused_moe
     E, H = w13.shape[0], w13.shape[2]
-    for T in (1, max_num_tokens):
-        x = torch.randn(T, H, device=w13.device, dtype=w13.dtype)
-        ids = torch.randint(0, E, (T, top_k), device=w13.device)
-        weights = torch.rand(T, top_k, device=w13.device)
-        fused_moe(x, w13, w2, weights, ids)
+    dev = w13.device
+    table = {}
+    T = 1
+    sizes = []
+    while T < max_num_tokens:
+        sizes.append(T)
+        T *= 2
+    sizes.append(max_num_tokens)
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    for T in sizes:
+        numel = T * top_k
+        x = torch.randn(T, H, device=dev, dtype=torch.bfloat16)
+        ids = torch.randint(0, E, (T, top_k), device=dev, dtype=torch.int32)
+        weights = torch.rand(T, top_k, device=dev)
+        best = None
+        for bm in _candidates(numel, E, packed):
+            set_moe_block_m(numel, numel, bm, packed)
+            if moe_block_m(T, H, w2.shape[-1], E, top_k, packed) != bm:
+                continue   # the shape has no kernel at this height
+            fn(x, w13, w2, weights, ids)  # warm-up
+            start.record()
+            for _ in range(reps):
+                fn(x, w13, w2, weights, ids)
+            stop.record()
+            stop.synchronize()
+            us = start.elapsed_time(stop) * 1e3 / reps
+            if best is None or us < best[1]:
+                best = (bm, us)
+        set_moe_block_m(numel, numel, best[0] if best else -1, packed)
+        if best:
+            table[1 << (numel.bit_length() - 1)] = best
+    return table
