@@ -14,6 +14,8 @@ Functions and the reference code they restate:
 - moe_align_block_size_np  tinykernels.py:1070-1190 (the torch moe_align_block_size).
 - sparse_moe_reference     serve.py:1076-1099 at TP=1 with TRITON_KERNELS off: gate Linear, route,
                                               moe_reference.
+- silu_and_mul_reference   tinykernels.py:293-297 / serve.py's F.silu(gate) * up in bf16: silu of
+                                              the fp32 gate rounded to bf16, times up, rounded.
 - add_rmsnorm_reference    serve.py:799-809 (RMSNorm, fp32) and 1185-1193 (add_rmsnorm: residual
                                               = residual + x in bf16, then the norm), with x the
                                               k-sum of the per-slot rows as tinykernels.py:1796
@@ -102,6 +104,11 @@ def moe_align_block_size_np(topk_ids, block_m, num_experts):
     expert_ids = np.where(expert_ids >= num_experts, -1, expert_ids).astype(np.int32)
     total = np.array([padded_end[-1] if nb else 0], dtype=np.int32)
     return sorted_ids, expert_ids, total
+
+
+def silu_and_mul_reference(gate, up):
+    s = F.silu(gate.float()).to(gate.dtype).float()
+    return (s * up.float()).to(gate.dtype)
 
 
 def add_rmsnorm_reference(rows, top_k, residual, weight, eps):

@@ -224,12 +224,17 @@ def test_graph_capture_replay(dev, tsm, qwen_layer):
 
 
 def test_silu_and_mul(dev, tsm):
+    """Against the oracle restatement (tinykernels.py:293-297): equal except where the kernel's
+    hardware sigmoid lands the rounded silu on the other side of a bf16 rounding boundary
+    (then within one bf16 ulp of the product)."""
+    from oracle.moe_oracle import silu_and_mul_reference
     g = torch.randn(300, 2 * 768, device=dev).bfloat16() * 3
     out = tsm.silu_and_mul(g[:, :768], g[:, 768:])
-    ref = (F.silu(g[:, :768].float()).bfloat16().float() * g[:, 768:].float()).bfloat16()
-    diff = (out.float() - ref.float()).abs()
+    ref = silu_and_mul_reference(g[:, :768].cpu(), g[:, 768:].cpu())
+    diff = (out.float().cpu() - ref.float()).abs()
     ulp = ref.float().abs().clamp_min(1e-30) * 2.0 ** -6  # two bf16 ulps
     assert bool((diff <= ulp + 1e-30).all())
+    assert (diff > 0).float().mean().item() < 1e-2
 
 
 def test_pack_layout_matches_definition(dev, tsm):

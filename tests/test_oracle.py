@@ -258,3 +258,17 @@ def test_add_rmsnorm_reference_known_answers():
     rows2 = torch.stack([torch.full((H,), 3.0), torch.full((H,), -3.0)]).bfloat16()
     out, res = add_rmsnorm_reference(rows2, 2, torch.ones(1, H).bfloat16(), w, 0.0)
     assert torch.equal(res, torch.ones(1, H).bfloat16()) and torch.equal(out[0], w)
+
+
+def test_silu_and_mul_reference():
+    from oracle.moe_oracle import silu_and_mul_reference
+    g = torch.tensor([0.0, 20.0, -20.0, 1.0, -1.0]).bfloat16()
+    u = torch.tensor([5.0, 2.0, 3.0, 1.0, 1.0]).bfloat16()
+    out = silu_and_mul_reference(g, u).double()
+    assert out[0] == 0 and abs(out[1] - 40.0) <= 0.25 and abs(out[2]) < 1e-6
+    x = torch.randn(1000, generator=torch.Generator().manual_seed(0)).bfloat16() * 4
+    y = torch.randn(1000, generator=torch.Generator().manual_seed(1)).bfloat16()
+    ref = x.double() / (1 + torch.exp(-x.double())) * y.double()
+    got = silu_and_mul_reference(x, y).double()
+    # two roundings to bf16 (silu, then the product): within 2^-7 relative
+    assert bool(((got - ref).abs() <= ref.abs() * 2.0 ** -7 + 1e-30).all())
