@@ -124,3 +124,21 @@ def test_plan_overrides(lib):
     assert lib.tsm_moe_set_block_m(1, 1 << 40, 1, -1) == 0
     assert lib.tsm_moe_block_m(64, 2048, 768, 128, 8, 0) == base
     assert lib.tsm_moe_set_block_m(0, 4, 0, 16) == -1       # numel_lo >= 1
+
+
+def test_attention_validation(lib):
+    """Head counts are checked before they are divided (a host-side UBSan run found H = 0
+    reaching a modulo by zero)."""
+    P, I64, I32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
+    f = lib.tsm_paged_attention
+    f.argtypes = [P, I64, I32, I64, I64, P, P, I64, I32, I32, I32, P, P, P, I64, I32, I32,
+                  ctypes.c_float, P, I64, I64, P]
+    args = lambda H, Hkv, D=128, page=16: (P(256), 4, H, H * D, D, P(256), P(256), 8, page,  # noqa
+                                            Hkv, D, P(256), P(256), P(256), 4, 2, 1, 0.1,
+                                            P(256), H * D, D, None)
+    assert f(*args(0, 4)) == -1
+    assert f(*args(32, 0)) == -1
+    assert f(*args(2, 4)) == -1           # fewer query heads than KV heads
+    assert f(*args(32 * 3, 3)) == -2      # group 32 does not divide 16
+    assert f(*args(32, 4, D=96)) == -2    # head_dim
+    assert f(*args(32, 4, page=6)) == -2  # page % 4

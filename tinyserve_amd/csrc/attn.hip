@@ -462,10 +462,10 @@ extern "C" int tsm_paged_attention(const void* q, int64_t T, int H, int64_t q_to
     clear_error();
     TSM_REQUIRE(T >= 0 && T <= 0x7fffffffll && num_seqs >= 0 && num_seqs <= 65535, TSM_E_ARG,
                 "bad sizes (T=%lld B=%d)", (long long)T, num_seqs);
-    TSM_REQUIRE(Hkv >= 1 && H % Hkv == 0, TSM_E_ARG, "H (%d) must be a multiple of Hkv (%d)", H,
-                Hkv);
+    TSM_REQUIRE(Hkv >= 1 && H >= Hkv && H % Hkv == 0, TSM_E_ARG,
+                "H (%d) must be a positive multiple of Hkv (%d)", H, Hkv);
     const int group = H / Hkv;
-    TSM_REQUIRE(group <= 16 && 16 % group == 0, TSM_E_SHAPE,
+    TSM_REQUIRE(group >= 1 && group <= 16 && 16 % group == 0, TSM_E_SHAPE,
                 "query heads per KV head must divide 16 (got %d)", group);
     TSM_REQUIRE(D == 64 || D == 128, TSM_E_SHAPE, "head_dim must be 64 or 128 (got %d)", D);
     TSM_REQUIRE(page >= 4 && page % 4 == 0, TSM_E_SHAPE, "page size must be a multiple of 4");
