@@ -477,6 +477,8 @@ extern "C" int tsm_paged_attention(const void* q, int64_t T, int H, int64_t q_to
     if (T == 0 || num_seqs == 0) return TSM_OK;
     TSM_REQUIRE(q && k_cache && v_cache && query_start_loc && cu_seqlens_k && block_table && out,
                 TSM_E_ARG, "null pointer argument");
+    TSM_REQUIRE(tsm_aligned(16, {q, k_cache}) && tsm_aligned(8, {v_cache, out}), TSM_E_ARG,
+                "attention needs 16-byte aligned q and K pages, 8-byte aligned V pages and out");
     AttnArgs a{};
     a.q = (const bf16_t*)q;
     a.k_cache = (const bf16_t*)k_cache;

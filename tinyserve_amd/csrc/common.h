@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <string.h>
+#include <initializer_list>
 
 namespace tsm {
 
@@ -148,6 +149,13 @@ int check_launch(const char* what);
 // hipGetLastError call cleared).
 int launch_status(hipError_t e, const char* what);
 }  // namespace tsm
+
+// True when every non-null pointer is a multiple of `a` bytes (the kernels' vector accesses).
+inline bool tsm_aligned(size_t a, std::initializer_list<const void*> ptrs) {
+    for (const void* p : ptrs)
+        if (p && (reinterpret_cast<uintptr_t>(p) % a) != 0) return false;
+    return true;
+}
 
 #define TSM_REQUIRE(cond, code, ...)          \
     do {                                       \

@@ -159,6 +159,8 @@ extern "C" int tsm_fused_moe_f32(const float* x, const float* w13, const float* 
     if (rc) return rc;
     if (T == 0) return TSM_OK;
     TSM_REQUIRE(x && w13 && w2 && topk_w && topk_ids && out, TSM_E_ARG, "null pointer argument");
+    TSM_REQUIRE(tsm_aligned(4, {x, w13, w2, topk_w, topk_ids, out}), TSM_E_ARG,
+                "fp32 tensors must be 4-byte aligned");
     const LayoutF32 L = layout_f32(T, H, I, E, top_k);
     TSM_REQUIRE(ws && ws_bytes >= L.bytes && ((uintptr_t)ws & 255) == 0, TSM_E_WORKSPACE,
                 "workspace must be 256-byte aligned and >= %zu bytes (got %zu)", L.bytes,

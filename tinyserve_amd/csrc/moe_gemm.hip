@@ -555,6 +555,8 @@ static int fused_moe_impl(const void* x, const void* w13, const void* w2, const 
     if (rc) return rc;
     if (T == 0) return TSM_OK;
     TSM_REQUIRE(x && w13 && w2 && topk_w && topk_ids && out, TSM_E_ARG, "null pointer argument");
+    TSM_REQUIRE(tsm_aligned(16, {x, w13, w2, out}), TSM_E_ARG,
+                "x, weights and out must be 16-byte aligned");
     const Layout L = layout_for(T, H, I, E, top_k, false);
     TSM_REQUIRE(ws && ws_bytes >= L.bytes && ((uintptr_t)ws & 255) == 0, TSM_E_WORKSPACE,
                 "workspace must be 256-byte aligned and >= %zu bytes (got %zu)", L.bytes,
@@ -594,6 +596,8 @@ static int moe_forward_impl(const void* x, const void* gate_w, const void* w13, 
     if (rc) return rc;
     if (T == 0) return TSM_OK;
     TSM_REQUIRE(x && gate_w && w13 && w2 && out, TSM_E_ARG, "null pointer argument");
+    TSM_REQUIRE(tsm_aligned(16, {x, gate_w, w13, w2, out}), TSM_E_ARG,
+                "x, weights and out must be 16-byte aligned");
     const Layout L = layout_for(T, H, I, E, top_k, true);
     TSM_REQUIRE(ws && ws_bytes >= L.bytes && ((uintptr_t)ws & 255) == 0, TSM_E_WORKSPACE,
                 "workspace must be 256-byte aligned and >= %zu bytes (got %zu)", L.bytes,

@@ -122,6 +122,8 @@ extern "C" int tsm_add_rmsnorm(const void* x, int64_t T, int H, int top_k, void*
     TSM_REQUIRE(!residual_in || residual, TSM_E_ARG, "residual_in needs a residual buffer");
     if (T == 0) return TSM_OK;
     TSM_REQUIRE(x && weight && out, TSM_E_ARG, "null pointer argument");
+    TSM_REQUIRE(tsm_aligned(16, {x, residual, weight, out}), TSM_E_ARG,
+                "add_rmsnorm needs 16-byte aligned tensors");
     const int cpr = H / 8;
     const bf16_t* xb = (const bf16_t*)x;
     bf16_t* rb = (bf16_t*)residual;

@@ -805,6 +805,7 @@ extern "C" int tsm_moe_router(const void* x, const void* gate_w, int dtype, int6
                 "router needs H %% 8 == 0 and 8 <= H <= 4096 (got %d)", H);
     if (T == 0) return TSM_OK;
     TSM_REQUIRE(x && gate_w && topk_w && topk_ids, TSM_E_ARG, "null pointer argument");
+    TSM_REQUIRE(tsm_aligned(16, {x, gate_w}), TSM_E_ARG, "x and gate_w must be 16-byte aligned");
     hipError_t err;
     if (dtype == TSM_BF16 && router_mfma_supported(T, H, E))
         err = launch_router_mfma(x, gate_w, T, H, E, top_k, renorm, expert_map, bias,
