@@ -1,0 +1,110 @@
+"""Builds the CPU emulation library of the product's kernels (TEST INFRASTRUCTURE ONLY).
+
+The product's tinyserve_amd/csrc/*.hip sources are compiled as host C++ against the stand-in HIP
+environment of tests/emu/emu_hip.h (fiber-per-thread execution, cross-lane operations and the
+matrix-core instruction evaluated on the CPU). Two textual adaptations are made on copies of the
+sources, never on the sources themselves: the dynamic LDS declaration becomes a pointer to the
+emulated LDS, and the two inline-assembly idioms the tile kernel uses (a register copy that
+places a wait, and an LDS-wait + workgroup barrier) become their host equivalents. Any other
+inline assembly stops the build.
+
+The result, tests/emu/_build/libtsm_emu[_asan].so, exports the same C ABI as
+libtinyserve_moe.so and is loaded only by tests (with `asan=True` the kernels' every memory
+access is checked by AddressSanitizer: the CPU counterpart of a GPU memory fault).
+"""
+import hashlib
+import os
+import re
+import shutil
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(os.path.dirname(HERE))
+CSRC = os.path.join(ROOT, "tinyserve_amd", "csrc")
+OUT = os.path.join(HERE, "_build")
+
+ASM_REWRITES = [
+    (re.compile(r'asm volatile\("v_mov_b32 %0, %1" : "=v"\((\w+)\) : "v"\((\w+)\)\);'),
+     r"\1 = \2;"),
+    (re.compile(r'asm volatile\("s_waitcnt lgkmcnt\(0\)\\n\\ts_barrier" ::: "memory"\);'),
+     "::emu::syncthreads();"),
+]
+LDS_DECL = re.compile(r"extern __shared__[^;]*\bchar (\w+)\[\];")
+
+
+def _clang():
+    for c in ("/opt/rocm/llvm/bin/clang++", shutil.which("clang++") or ""):
+        if c and os.path.exists(c):
+            return c
+    raise RuntimeError("clang++ not found")
+
+
+def adapt(text: str, name: str) -> str:
+    text = LDS_DECL.sub(r"char* const \1 = ::emu::dynamic_lds();", text)
+    for pat, rep in ASM_REWRITES:
+        text = pat.sub(rep, text)
+    if re.search(r"\b(asm|__asm__)\s*(volatile\s*)?\(", text):
+        raise RuntimeError(f"{name}: inline assembly the emulator does not know")
+    return text
+
+
+def sources():
+    return sorted(f for f in os.listdir(CSRC) if f.endswith(".hip"))
+
+
+def build(asan: bool = False, jobs: int = 8) -> str:
+    tag = "_asan" if asan else ""
+    lib = os.path.join(OUT, f"libtsm_emu{tag}.so")
+    h = hashlib.sha256()
+    inputs = [os.path.join(CSRC, f) for f in sources()] + [
+        os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".h")] + [
+        os.path.join(HERE, "emu_hip.h"), os.path.join(HERE, "emu_runtime.cpp"),
+        os.path.join(ROOT, "include", "tinyserve_moe.h"), os.path.abspath(__file__)]
+    for p in sorted(inputs):
+        h.update(open(p, "rb").read())
+    stamp = lib + ".sha256"
+    if os.path.exists(lib) and os.path.exists(stamp) and open(stamp).read() == h.hexdigest():
+        return lib
+    src_dir = os.path.join(OUT, "src")
+    obj_dir = os.path.join(OUT, f"obj{tag}")
+    os.makedirs(src_dir, exist_ok=True)
+    os.makedirs(obj_dir, exist_ok=True)
+    flags = ["-std=c++17", "-O1", "-g", "-fPIC", "-fno-omit-frame-pointer", "-w",
+             f"-I{os.path.join(HERE, 'include')}", f"-I{os.path.join(ROOT, 'include')}",
+             f"-I{CSRC}", "-include", os.path.join(HERE, "emu_hip.h")]
+    if asan:
+        flags += ["-fsanitize=address,undefined", "-fno-sanitize-recover=undefined"]
+    units = []
+    for f in sources():
+        dst = os.path.join(src_dir, f[:-4] + ".cpp")
+        text = adapt(open(os.path.join(CSRC, f)).read(), f)
+        if not os.path.exists(dst) or open(dst).read() != text:
+            open(dst, "w").write(text)
+        units.append(dst)
+    units.append(os.path.join(HERE, "emu_runtime.cpp"))
+    cxx = _clang()
+
+    def compile_one(src):
+        obj = os.path.join(obj_dir, os.path.basename(src) + ".o")
+        r = subprocess.run([cxx, *flags, "-c", src, "-o", obj], capture_output=True, text=True)
+        if r.returncode:
+            raise RuntimeError(f"emulation build of {src} failed:\n{r.stderr[-4000:]}")
+        return obj
+
+    with ThreadPoolExecutor(max_workers=jobs) as ex:
+        objs = list(ex.map(compile_one, units))
+    link = [cxx, "-shared", "-o", lib + ".tmp", *objs]
+    if asan:
+        link.insert(1, "-fsanitize=address,undefined")
+    r = subprocess.run(link, capture_output=True, text=True)
+    if r.returncode:
+        raise RuntimeError(f"emulation link failed:\n{r.stderr[-4000:]}")
+    os.replace(lib + ".tmp", lib)
+    open(stamp, "w").write(h.hexdigest())
+    return lib
+
+
+if __name__ == "__main__":
+    print(build(asan="--asan" in sys.argv))

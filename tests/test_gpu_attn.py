@@ -2,15 +2,26 @@
 serve.py's RMSNorm / rotary / torch_ref_attention (oracle/attn_oracle.py).
 
 Tolerances: q/k norm + RoPE within one bf16 ulp of the oracle (the kernel's reciprocal square
-root differs from torch's); attention outputs within 1e-2 absolute (outputs are convex
-combinations of V rows of magnitude ~1; the probabilities enter the P.V product in bf16, as in
-the reference's Triton kernel); argmax exact."""
+root differs from torch's); attention outputs within 8e-3 + 2^-7 |ref| (outputs are convex
+combinations of V rows of magnitude ~1, the probabilities enter the P.V product in bf16 as in
+the reference's Triton kernel, and the output itself is rounded to bf16: half an ulp of a value
+near 2 is already 2^-8); argmax exact."""
+
 import pytest
 import torch
 
 from oracle.attn_oracle import paged_attention_ref, qk_norm_rope_ref
 
 pytestmark = pytest.mark.gpu
+
+
+def attn_close(out, ref, what=""):
+    out, ref = out.float().cpu(), ref.float().cpu()
+    assert torch.isfinite(out).all(), what
+    err = (out - ref).abs()
+    bound = 8e-3 + ref.abs() * 2.0 ** -7
+    print(f"  {what} max abs err {err.max().item():.3e}", flush=True)
+    assert bool((err <= bound).all()), (what, float((err / bound).max()))
 
 
 def ulp_close(out, ref):
@@ -77,11 +88,7 @@ def test_paged_attention_against_oracle(dev, H, Hkv, D, page, q_lens, kv_lens):
     meta = Meta(dev, qsl, kv_lens, bt)
     out = paged_attention(q.to(dev), cache, meta, D ** -0.5)
     ref = paged_attention_ref(q.float(), kc.float(), vc.float(), qsl, kv_lens, bt, D ** -0.5)
-    out = out.float().cpu()
-    assert torch.isfinite(out[:qsl[-1]]).all()
-    err = (out - ref).abs().max().item()
-    print(f"  max abs err {err:.3e}", flush=True)
-    assert err <= 1e-2
+    attn_close(out, ref, "paged attention")
 
 
 def test_paged_attention_graph_replay(dev):
@@ -113,7 +120,7 @@ def test_paged_attention_graph_replay(dev):
     graph.replay()
     torch.cuda.synchronize()
     ref = paged_attention_ref(q.float(), kc.float(), vc.float(), qsl, kv2, bt, D ** -0.5)
-    assert (out.float().cpu() - ref).abs().max().item() <= 1e-2
+    attn_close(out, ref, "replay with shorter contexts")
 
 
 @pytest.mark.parametrize("T,H,Hkv,D", [(5, 32, 4, 128), (300, 8, 2, 64), (1, 4, 4, 128)])

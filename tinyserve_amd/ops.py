@@ -424,20 +424,24 @@ def _norm_impl(x, top_k, residual, residual_in, weight, eps):
     return out
 
 
-@torch.library.custom_op("tinyserve_amd::rmsnorm", mutates_args=("residual",))
-def rmsnorm(x: Tensor, weight: Tensor, eps: float,
-            residual: Optional[Tensor] = None) -> Tensor:
+@torch.library.custom_op("tinyserve_amd::add_rmsnorm", mutates_args=("residual",))
+def _add_rmsnorm(x: Tensor, top_k: int, residual: Optional[Tensor], residual_in: bool,
+                 weight: Tensor, eps: float) -> Tensor:
+    return _norm_impl(x, top_k, residual, residual_in, weight, eps)
+
+
+@_add_rmsnorm.register_fake
+def _(x, top_k, residual, residual_in, weight, eps):
+    H = x.shape[-1]
+    return x.new_empty(x.numel() // H // top_k, H)
+
+
+def rmsnorm(x: Tensor, weight: Tensor, eps: float, residual: Optional[Tensor] = None) -> Tensor:
     """tinykernels.rmsnorm (tinykernels.py:63-105): out = rmsnorm(x) * weight, or with a residual
     `residual += x` (rounded to bf16) then out = rmsnorm(residual) * weight, in one launch."""
-    return _norm_impl(x, 1, residual, residual is not None, weight, eps).view(x.shape)
+    return _add_rmsnorm(x, 1, residual, residual is not None, weight, eps).view(x.shape)
 
 
-@rmsnorm.register_fake
-def _(x, weight, eps, residual=None):
-    return torch.empty_like(x)
-
-
-@torch.library.custom_op("tinyserve_amd::moe_combine_add_rmsnorm", mutates_args=("residual",))
 def moe_combine_add_rmsnorm(rows: Tensor, top_k: int, residual: Tensor, weight: Tensor,
                             eps: float, residual_in: bool = True) -> Tensor:
     """The MoE block's k-sum fused into the next residual-add RMSNorm: rows [T*k, H] (fused_moe
@@ -445,10 +449,4 @@ def moe_combine_add_rmsnorm(rows: Tensor, top_k: int, residual: Tensor, weight: 
     residual = bf16(sum_k rows)), returns rmsnorm(residual) * weight [T, H]."""
     if residual is None:
         raise ValueError("moe_combine_add_rmsnorm needs a residual buffer")
-    return _norm_impl(rows, top_k, residual, residual_in, weight, eps)
-
-
-@moe_combine_add_rmsnorm.register_fake
-def _(rows, top_k, residual, weight, eps, residual_in=True):
-    H = rows.shape[-1]
-    return rows.new_empty(rows.numel() // H // top_k, H)
+    return _add_rmsnorm(rows, top_k, residual, residual_in, weight, eps)
