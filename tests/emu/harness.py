@@ -84,13 +84,16 @@ def asan_runtime():
     return found[-1] if found else None
 
 
-def run_under_asan(test_file: str, timeout: int = 900):
-    """pytest on `test_file` in a child process with the ASan runtime preloaded and
-    TSM_EMU_ASAN=1 (the tests then use the ASan build). Returns the CompletedProcess."""
+def run_under_asan(test_file: str, timeout: int = 900, select: str = None):
+    """pytest on `test_file` (optionally `-k select`) in a child process with the ASan runtime
+    preloaded and TSM_EMU_ASAN=1 (the tests then use the ASan build). Returns the
+    CompletedProcess."""
     rt = asan_runtime()
     env = dict(os.environ, TSM_EMU_ASAN="1", LD_PRELOAD=rt or "",
                ASAN_OPTIONS="detect_leaks=0:halt_on_error=1:abort_on_error=1",
                UBSAN_OPTIONS="halt_on_error=1:print_stacktrace=1")
-    return subprocess.run([sys.executable, "-m", "pytest", "-x", "-q", "-p", "no:cacheprovider",
-                           test_file], cwd=ROOT, env=env, capture_output=True, text=True,
+    cmd = [sys.executable, "-m", "pytest", "-x", "-q", "-p", "no:cacheprovider", test_file]
+    if select:
+        cmd += ["-k", select]
+    return subprocess.run(cmd, cwd=ROOT, env=env, capture_output=True, text=True,
                           timeout=timeout)

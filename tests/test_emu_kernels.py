@@ -1,0 +1,230 @@
+"""The product's kernels executed on the CPU (tests/emu: the HIP sources compiled as host C++
+against a fiber-per-thread device stand-in) through the product's own Python ops, against the
+oracles, at small sizes.
+
+What this pins: the kernels' indexing, data movement, masking, plans, padding and orchestration
+(the CPU build runs the same source); bit-exact where the arithmetic is exactly specified
+(routing, the permutation, the fixed-order router, residual streams, packing). What it does not:
+the GPU's own arithmetic (the matrix-core instruction is evaluated in double precision here) and
+anything about timing, memory ordering between workgroups or the compiler's device code
+generation. The -m gpu tests remain the parity tests proper.
+
+The same cases also run under AddressSanitizer (test_emu_asan.py) so that any out-of-bounds
+access of a kernel is caught on the CPU."""
+import os
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(HERE, "emu"))
+sys.path.insert(0, HERE)
+
+import harness  # noqa: E402
+from oracle import c_oracle  # noqa: E402
+from oracle.moe_oracle import (add_rmsnorm_reference, make_layer,  # noqa: E402
+                               moe_align_block_size_np, moe_reference)
+
+ASAN = os.environ.get("TSM_EMU_ASAN") == "1"
+
+
+@pytest.fixture(scope="module")
+def tsm():
+    import tinyserve_amd
+    with harness.emulated(asan=ASAN):
+        yield tinyserve_amd
+
+
+def bits(t):
+    return t.contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def same_bits(a, b):
+    return np.array_equal(np.asarray(a, np.float32).view(np.uint32),
+                          np.asarray(b, np.float32).view(np.uint32))
+
+
+def close(out, ref, max_abs=2e-2, mean_rel=5e-3):
+    out, ref = out.float(), ref.float()
+    assert torch.isfinite(out).all()
+    assert (out - ref).abs().max().item() <= max_abs
+    assert ((out - ref).abs().mean() / ref.abs().mean()).item() <= mean_rel
+
+
+@pytest.mark.parametrize("T,E,k", [(1, 128, 8), (33, 60, 4), (7, 512, 8), (64, 8, 2)])
+def test_route_bitexact(tsm, T, E, k):
+    g = torch.Generator().manual_seed(T + E)
+    logits = torch.randn(T, E, generator=g) * 2
+    logits[0, ::3] = 1.0                                 # ties
+    w, ids = tsm.moe_route(logits, k, True, None)
+    ow, oids = c_oracle.route(logits.numpy(), k, True)
+    assert np.array_equal(ids.numpy(), oids) and same_bits(w.numpy(), ow)
+
+
+@pytest.mark.parametrize("T", [3, 64, 300])
+def test_router_fused(tsm, T):
+    """T <= 256: the fixed-order kernels, bit-exact with the C oracle; T > 256: the matrix-core
+    router, its logits within the fp32 accumulation bound and its selection bit-exact."""
+    x, gw, _, _ = make_layer(T, 256, 16, 64, torch.bfloat16, seed=T)
+    w, ids, logits = tsm.moe_router(x, gw, 4, True)
+    if T <= 256:
+        ol = c_oracle.router_logits(bits(x), bits(gw))
+        assert same_bits(logits.numpy(), ol)
+    else:
+        exact = x.double() @ gw.double().t()
+        bound = (x.double().abs() @ gw.double().abs().t()) * 2.0 ** -17
+        assert bool(((logits.double() - exact).abs() <= bound).all())
+        ol = logits.numpy()
+    ow, oids = c_oracle.route(ol, 4, True)
+    assert np.array_equal(ids.numpy(), oids) and same_bits(w.numpy(), ow)
+
+
+@pytest.mark.parametrize("numel,E,bm", [(0, 8, 16), (37, 8, 16), (300, 16, 64), (9000, 32, 64)])
+def test_align_bitexact(tsm, numel, E, bm):
+    g = torch.Generator().manual_seed(numel)
+    ids = torch.randint(-1, E, (numel,), generator=g, dtype=torch.int32)
+    s, e, t = tsm.moe_align_block_size(ids, bm, E)
+    rs, re_, rt = moe_align_block_size_np(ids.numpy(), bm, E)
+    assert np.array_equal(s.numpy(), rs) and np.array_equal(e.numpy(), re_)
+    assert int(t[0]) == int(rt[0])
+
+
+@pytest.mark.parametrize("T", [2, 40, 300])
+def test_experts_every_plan(tsm, T):
+    """Every plan the static table or the tuner can pick (expert-major, 16-, 64-row tiles;
+    128-row persistent tiles on packed weights), both weight layouts, against the oracle; the
+    packed and reference-layout kernels of a plan agree bit for bit."""
+    from tinyserve_amd import kernels
+    H, E, I, k = 256, 8, 512, 2
+    x, gw, w13, w2 = make_layer(T, H, E, I, torch.bfloat16, seed=10 + T)
+    w, ids, _ = tsm.moe_router(x, gw, k, True)
+    ref = moe_reference(x, w13, w2, w, ids.long())
+    p13, p2 = tsm.pack_moe_weights(w13, w2)
+    numel = T * k
+    try:
+        for bm in (0, 16, 64, 128):
+            for packed in (False, True):
+                if bm == 128 and not packed:
+                    continue
+                kernels.set_moe_block_m(numel, numel, bm, packed)
+                if kernels.moe_block_m(T, H, I, E, k, packed) != bm:
+                    continue
+                out = (tsm.fused_moe_packed(x, p13, p2, w, ids) if packed
+                       else tsm.fused_moe(x, w13, w2, w, ids))
+                close(out, ref)
+                if packed and bm != 128:
+                    kernels.set_moe_block_m(numel, numel, bm, False)
+                    assert torch.equal(out, tsm.fused_moe(x, w13, w2, w, ids)), bm
+    finally:
+        kernels.set_moe_block_m(1, 1 << 30, -1, False)
+        kernels.set_moe_block_m(1, 1 << 30, -1, True)
+
+
+def test_expert_parallel_and_rows(tsm):
+    H, E, I, k, T = 256, 16, 128, 4, 50
+    x, gw, w13, w2 = make_layer(T, H, E, I, torch.bfloat16, seed=3)
+    emap = torch.arange(E, dtype=torch.int64)
+    emap[::2] = -1
+    w, ids, _ = tsm.moe_router(x, gw, k, True, emap)
+    assert bool((ids < 0).any())
+    out = tsm.fused_moe(x, w13, w2, w, ids)
+    close(out, moe_reference(x, w13, w2, w, ids.long()))
+    rows = tsm.fused_moe(x, w13, w2, w, ids, sum_topk=False).view(T, k, H)
+    assert bool((rows[ids < 0] == 0).all())
+    assert torch.equal(rows.float().sum(1).bfloat16(), out)
+
+
+def test_padded_shapes(tsm):
+    """I = 96 (the TP-8 share of Qwen3-30B-A3B) and H = 200 through the zero-padded packing."""
+    from tinyserve_amd import layout
+    x, gw, w13, w2 = make_layer(40, 256, 16, 96, torch.bfloat16, seed=2)
+    p13, p2 = tsm.pack_moe_weights(w13, w2)
+    assert torch.equal(p13, layout.pack(w13, True, 256, 256))
+    assert torch.equal(p2, layout.pack(w2, False, 256, 128))
+    w, ids, _ = tsm.moe_router(x, gw, 4, True)
+    out = tsm.fused_moe(x, w13, w2, w, ids)
+    close(out, moe_reference(x, w13, w2, w, ids.long()))
+    assert torch.equal(tsm.fused_moe_packed(x, p13, p2, w, ids), out)
+    x, gw, w13, w2 = make_layer(9, 200, 16, 50, torch.bfloat16, seed=3)
+    out = tsm.moe_forward(x, gw, w13, w2, 4, True)
+    assert out.shape == (9, 200)
+    w, ids, _ = tsm.moe_router(x, gw, 4, True)
+    close(out, moe_reference(x, w13, w2, w, ids.long()))
+
+
+def test_fp32_layer(tsm):
+    from oracle.moe_oracle import per_token_fp64
+    x, gw, w13, w2 = make_layer(20, 256, 8, 512, torch.float32, seed=0)
+    w, ids, _ = tsm.moe_router(x, gw, 2, True)
+    out = tsm.fused_moe(x, w13, w2, w, ids)
+    assert out.dtype == torch.float32
+    r64 = per_token_fp64(x, w13, w2, w, ids.long())
+    assert torch.allclose(out.double(), r64, atol=2e-6, rtol=1e-4)
+
+
+@pytest.mark.parametrize("k,H", [(1, 256), (8, 256), (2, 4096), (1, 200)])
+def test_add_rmsnorm(tsm, k, H):
+    g = torch.Generator().manual_seed(k * H)
+    rows = torch.randn(7 * k, H, generator=g).bfloat16()
+    res = torch.randn(7, H, generator=g).bfloat16()
+    nw = (1 + 0.1 * torch.randn(H, generator=g)).bfloat16()
+    r = res.clone()
+    out = tsm.ops.moe_combine_add_rmsnorm(rows, k, r, nw, 1e-6)
+    ref, ref_res = add_rmsnorm_reference(rows, k, res, nw, 1e-6)
+    assert torch.equal(r, ref_res)
+    ulp = torch.exp2(torch.floor(torch.log2(ref.float().abs().clamp_min(2.0 ** -126))) - 7)
+    assert bool(((out.float() - ref.float()).abs() <= ulp).all())
+    if k == 1:   # without a residual: the norm of the rows themselves
+        plain = tsm.ops.rmsnorm(rows, nw, 1e-6)
+        pref = add_rmsnorm_reference(rows, 1, None, nw, 1e-6)[0]
+        ulp = torch.exp2(torch.floor(torch.log2(pref.float().abs().clamp_min(2.0 ** -126))) - 7)
+        assert bool(((plain.float() - pref.float()).abs() <= ulp).all())
+
+
+def test_attention_side(tsm):
+    from oracle.attn_oracle import paged_attention_ref, qk_norm_rope_ref
+    from test_gpu_attn import Meta, build_batch
+    from tinyserve_amd.attention import (PagedKVCache, greedy_argmax, paged_attention,
+                                         qk_norm_rope)
+    for H, Hkv, D, page, ql, kl in [(32, 4, 128, 16, [1, 1, 3, 0], [1, 33, 40, 0]),
+                                    (8, 4, 64, 8, [3, 1, 17, 2], [9, 129, 17, 2]),
+                                    (16, 1, 128, 32, [7, 1], [100, 300])]:
+        q, kc, vc, cache, bt, qsl = build_batch("cpu", ql, kl, H, Hkv, D, page, seed=H + D)
+        out = paged_attention(q, cache, Meta("cpu", qsl, kl, bt), D ** -0.5).float()
+        ref = paged_attention_ref(q.float(), kc.float(), vc.float(), qsl, kl, bt, D ** -0.5)
+        assert torch.isfinite(out).all()
+        assert bool(((out - ref).abs() <= 8e-3 + ref.abs() * 2.0 ** -7).all())
+    T, H, Hkv, D = 5, 8, 2, 64
+    g = torch.Generator().manual_seed(1)
+    qkv = (torch.randn(T, (H + 2 * Hkv) * D, generator=g) * 3).bfloat16()
+    ang = torch.rand(T, D // 2, generator=g) * 5
+    qw = (1 + 0.1 * torch.randn(D, generator=g)).bfloat16()
+    kw = (1 + 0.1 * torch.randn(D, generator=g)).bfloat16()
+    q, k, v = (t.reshape(T, -1, D) for t in qkv.split([H * D, Hkv * D, Hkv * D], -1))
+    rq, rk = qk_norm_rope_ref(q, k, ang.cos(), ang.sin(), qw, kw, 1e-6)
+    d = qkv.clone()
+    dq, dk, dv = (t.view(T, -1, D) for t in d.split([H * D, Hkv * D, Hkv * D], -1))
+    cache = PagedKVCache.allocate(4, 16, Hkv, D, "cpu")
+    slots = torch.tensor([16, 17, 40, -1, 6000])          # -1 and past the pool: not written
+    qk_norm_rope(dq, dk, ang.cos(), ang.sin(), qw, kw, 1e-6, dv, cache, slots)
+    assert torch.equal(dq, rq) and torch.equal(dk, rk)
+    assert torch.equal(cache.k[1, 0], dk[0]) and torch.equal(cache.v[2, :, :, 8], v[2])
+    x = torch.randn(6, 1000, generator=g)
+    x[2, 5] = x[2, 900] = 99.0
+    assert torch.equal(greedy_argmax(x), x.argmax(-1))
+
+
+def test_end_to_end_driver(tsm):
+    """The qwen3_moe driver (prefill, then decode steps) on a two-layer model: its greedy tokens
+    equal the decoder oracle's wherever the oracle's top two logits are apart."""
+    from test_gpu_e2e import reference_logits, small_cfg
+    from tinyserve_amd.e2e import build_model, generate
+    model = build_model(small_cfg(), device="cpu", seed=3, router_logits="fp32")
+    prompts = torch.randint(0, 1000, (2, 20), generator=torch.Generator().manual_seed(7))
+    toks, _, _ = generate(model, prompts, 4, graph=False)
+    steps = reference_logits(model, torch.cat([prompts, toks[:, :-1]], 1))[:, 19:]
+    top2 = steps.topk(2, dim=-1).values
+    clear = (top2[..., 0] - top2[..., 1]) > 3e-2 * steps.abs().max()
+    assert bool((toks == steps.argmax(-1))[clear].all())
