@@ -142,3 +142,21 @@ def test_attention_validation(lib):
     assert f(*args(32 * 3, 3)) == -2      # group 32 does not divide 16
     assert f(*args(32, 4, D=96)) == -2    # head_dim
     assert f(*args(32, 4, page=6)) == -2  # page % 4
+
+
+def test_128_row_plan_only_where_the_tile_kernels_run(lib):
+    I32, I64, P = ctypes.c_int, ctypes.c_int64, ctypes.c_void_p
+    lib.tsm_moe_block_m.argtypes = [I64, I32, I32, I32, I32, I32]
+    assert lib.tsm_moe_block_m(8192, 2048, 768, 128, 8, 1) == 128
+    assert lib.tsm_moe_block_m(8192, 128, 64, 32, 8, 1) == 64      # 2I % 256 != 0
+    assert lib.tsm_moe_block_m(8192, 2176, 768, 32, 8, 1) == 64    # H % 256 != 0
+    lib.tsm_moe_set_block_m.argtypes = [I64, I64, I32, I32]
+    assert lib.tsm_moe_set_block_m(1, 1 << 30, 1, 128) == 0
+    assert lib.tsm_moe_block_m(64, 128, 64, 32, 8, 1) == 64        # installed 128 not taken
+    assert lib.tsm_moe_set_block_m(1, 1 << 30, 1, -1) == 0
+    f = lib.tsm_moe_gemm_gate_up
+    f.argtypes = [P, P, P, P, P, I64, I32, I32, I32, I32, I32, I32, P, P]
+    lib.tsm_last_error.restype = ctypes.c_char_p
+    assert f(P(256), P(256), P(256), P(256), P(256), 512, 8, 128, 64, 32, 128, 1, P(256),
+             None) == -2
+    assert b"128-row" in lib.tsm_last_error()

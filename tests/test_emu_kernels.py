@@ -228,3 +228,21 @@ def test_end_to_end_driver(tsm):
     top2 = steps.topk(2, dim=-1).values
     clear = (top2[..., 0] - top2[..., 1]) > 3e-2 * steps.abs().max()
     assert bool((toks == steps.argmax(-1))[clear].all())
+
+
+def test_packed_prefill_without_tile_kernels(tsm):
+    """A layer the 128-row tile kernels do not take (2I % 256 != 0 here: H = 128, I = 64) at a
+    prefill size: the plan must stay at 64-row tiles. (It once chose 128-row tiles whatever the
+    shape, and the 64-row fallback kernel then read the 128-row permutation as 64-row tiles.)"""
+    from tinyserve_amd import kernels
+    T, H, E, I, k = 513, 128, 32, 64, 8
+    assert kernels.moe_block_m(T, H, I, E, k, True) == 64
+    x, gw, w13, w2 = make_layer(T, H, E, I, torch.bfloat16, seed=T)
+    bias = torch.zeros(E)
+    bias[E // 2:] = float("-inf")
+    w, ids, _ = tsm.moe_router(x, gw, k, True, None, bias)
+    p13, p2 = tsm.pack_moe_weights(w13, w2)
+    out = tsm.fused_moe_packed(x, p13, p2, w, ids)
+    assert torch.equal(out, tsm.fused_moe(x, w13, w2, w, ids))
+    sel = slice(0, 64)
+    close(out[sel], moe_reference(x[sel], w13, w2, w[sel], ids[sel].long()))

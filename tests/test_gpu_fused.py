@@ -462,3 +462,19 @@ def test_autotune_installs_plans(dev, tsm, qwen_layer):
         assert_close(tsm.fused_moe(x, w13, w2, w, ids), ref, f"autotuned T={T} bm={bm}")
     kernels.set_moe_block_m(1, 1 << 30, -1)
     assert {T: kernels.moe_block_m(T, 2048, 768, 128, 8) for T in (1, 64, 512)} == before
+
+
+def test_packed_prefill_without_tile_kernels(dev, tsm):
+    """A layer the 128-row tile kernels do not take (H = 128, I = 64: 2I % 256 != 0) at a
+    prefill size runs 64-row tiles on packed weights and matches the reference layout and the
+    oracle (the plan once chose 128-row tiles whatever the shape)."""
+    from oracle.moe_oracle import make_layer
+    T, H, E, I, k = 1500, 128, 32, 64, 8
+    x, gw, w13, w2 = make_layer(T, H, E, I, torch.bfloat16, seed=T, device=dev)
+    w, ids, _ = tsm.moe_router(x, gw, k, True)
+    p13, p2 = tsm.pack_moe_weights(w13, w2)
+    out = tsm.fused_moe_packed(x, p13, p2, w, ids)
+    assert torch.equal(out, tsm.fused_moe(x, w13, w2, w, ids))
+    sel = torch.arange(0, T, 5)
+    ref = moe_reference(x.cpu()[sel], w13.cpu(), w2.cpu(), w.cpu()[sel], ids.cpu().long()[sel])
+    assert_close(out.cpu()[sel], ref, "H=128 I=64 packed prefill")

@@ -47,6 +47,8 @@ inline int64_t active_tile_bound(int64_t numel, int E, int block_m) {
 }
 
 // LDS-pipelined kernels for 64/128-row tiles on packed weights; false if unsupported.
+// tile_kernels_take: whether they take an (H, I) layer (the 128-row plan exists only then).
+bool tile_kernels_take(int H, int I);
 bool launch_tile_gate_up(GemmArgs g, int block_m, hipStream_t stream);
 bool launch_tile_down(GemmArgs g, int block_m, hipStream_t stream);
 

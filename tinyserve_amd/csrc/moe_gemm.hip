@@ -286,12 +286,14 @@ Plan plan_for(int64_t T, int H, int I, int E, int top_k, bool packed) {
         const int o = g_block_m_override[packed][numel_bucket(numel)].load(std::memory_order_relaxed);
         // an installed height applies where its kernels take the shape
         if (o == 0 && expert_path_supported(numel, H, I, E)) return Plan{0};
-        if (o > 0 && block_m_supported(o, packed)) return Plan{o};
+        if (o > 0 && block_m_supported(o, packed) && (o != 128 || tile_kernels_take(H, I)))
+            return Plan{o};
     }
     if (numel >= 1 && numel <= 12ll * E && expert_path_supported(numel, H, I, E))
         return Plan{0};
     if (numel <= 4ll * E) return Plan{16};
-    if (!packed || numel <= 32ll * E) return Plan{64};
+    // 128-row tiles exist only as the pipelined tile kernels, which need their shapes
+    if (!packed || numel <= 32ll * E || !tile_kernels_take(H, I)) return Plan{64};
     return Plan{128};
 }
 
@@ -385,31 +387,37 @@ void launch_lds(const GemmArgs& g, bool packed, hipStream_t stream) {
                            stream, g);
 }
 
-void launch_gate_up(const bf16_t* x, const bf16_t* w13, const int32_t* sorted,
+// false: no kernel for this tile height and shape (nothing launched). 128-row tiles have only the
+// pipelined tile kernel; 16 and 64 fall back to the LDS kernel of their own height.
+bool launch_gate_up(const bf16_t* x, const bf16_t* w13, const int32_t* sorted,
                     const int32_t* eids, const int32_t* total, int64_t numel, int top_k, int H,
                     int I, int E, int block_m, bool packed, bf16_t* act, hipStream_t stream) {
     GemmArgs g = gemm_args(x, w13, act, nullptr, sorted, eids, total, numel, top_k, I, H, E,
                            block_m, I / (kBN / 2));
-    if (block_m == 16 && launch_stream_gate_up(g, packed, stream)) return;
-    if (packed && block_m >= 64 && launch_tile_gate_up(g, block_m, stream)) return;
+    if (block_m == 16 && launch_stream_gate_up(g, packed, stream)) return true;
+    if (packed && block_m >= 64 && launch_tile_gate_up(g, block_m, stream)) return true;
+    if (block_m != 16 && block_m != 64) return false;
     if (block_m == 16)
         launch_lds<16, 1, 4, true>(g, packed, stream);
     else
         launch_lds<64, 2, 2, true>(g, packed, stream);
+    return true;
 }
 
 // down GEMM * routing weight: rows[numel, H] from act[max_padded, I] and w2[E, H, I].
-void launch_down(const bf16_t* act, const bf16_t* w2, const float* topk_w, const int32_t* sorted,
+bool launch_down(const bf16_t* act, const bf16_t* w2, const float* topk_w, const int32_t* sorted,
                  const int32_t* eids, const int32_t* total, int64_t numel, int H, int I, int E,
                  int block_m, bool packed, bf16_t* rows, hipStream_t stream) {
     GemmArgs g = gemm_args(act, w2, rows, topk_w, sorted, eids, total, numel, 1, H, I, E,
                            block_m, H / kBN);
-    if (block_m == 16 && launch_stream_down(g, packed, stream)) return;
-    if (packed && block_m >= 64 && launch_tile_down(g, block_m, stream)) return;
+    if (block_m == 16 && launch_stream_down(g, packed, stream)) return true;
+    if (packed && block_m >= 64 && launch_tile_down(g, block_m, stream)) return true;
+    if (block_m != 16 && block_m != 64) return false;
     if (block_m == 16)
         launch_lds<16, 1, 4, false>(g, packed, stream);
     else
         launch_lds<64, 2, 2, false>(g, packed, stream);
+    return true;
 }
 
 void launch_combine(const bf16_t* rows, int64_t T, int H, int top_k, bf16_t* out,
@@ -487,10 +495,11 @@ int run_experts(const void* x, const void* w13, const void* w2, const float* top
         launch_align(topk_ids, numel, E, pl.block_m, sorted, eids, total, ws + L.hist, stream),
         "fused_moe align kernels");
     if (rc) return rc;
-    launch_gate_up((const bf16_t*)x, (const bf16_t*)w13, sorted, eids, total, numel, top_k, H, I,
-                   E, pl.block_m, packed, act, stream);
-    launch_down(act, (const bf16_t*)w2, topk_w, sorted, eids, total, numel, H, I, E, pl.block_m,
-                packed, rows, stream);
+    TSM_REQUIRE(launch_gate_up((const bf16_t*)x, (const bf16_t*)w13, sorted, eids, total, numel,
+                               top_k, H, I, E, pl.block_m, packed, act, stream) &&
+                    launch_down(act, (const bf16_t*)w2, topk_w, sorted, eids, total, numel, H, I,
+                                E, pl.block_m, packed, rows, stream),
+                TSM_E_SHAPE, "internal: no %d-row kernel for H=%d I=%d", pl.block_m, H, I);
     if (sum_topk) launch_combine(rows, T, H, top_k, (bf16_t*)out, stream);
     return check_launch("fused_moe kernels");
 }
@@ -645,8 +654,10 @@ extern "C" int tsm_moe_gemm_gate_up(const void* x, const void* w13, const int32_
     if (numel == 0) return TSM_OK;
     TSM_REQUIRE(x && w13 && sorted_ids && expert_ids && total && act, TSM_E_ARG,
                 "null pointer argument");
-    launch_gate_up((const bf16_t*)x, (const bf16_t*)w13, sorted_ids, expert_ids, total, numel,
-                   top_k, H, I, E, block_m, weight_layout != 0, (bf16_t*)act, stream);
+    TSM_REQUIRE(launch_gate_up((const bf16_t*)x, (const bf16_t*)w13, sorted_ids, expert_ids,
+                               total, numel, top_k, H, I, E, block_m, weight_layout != 0,
+                               (bf16_t*)act, stream),
+                TSM_E_SHAPE, "no %d-row gate_up kernel for H=%d I=%d", block_m, H, I);
     return check_launch("gate_up GEMM");
 }
 
@@ -663,8 +674,10 @@ extern "C" int tsm_moe_gemm_down(const void* act, const void* w2, const float* t
     if (numel == 0) return TSM_OK;
     TSM_REQUIRE(act && w2 && topk_w && sorted_ids && expert_ids && total && rows, TSM_E_ARG,
                 "null pointer argument");
-    launch_down((const bf16_t*)act, (const bf16_t*)w2, topk_w, sorted_ids, expert_ids, total,
-                numel, H, I, E, block_m, weight_layout != 0, (bf16_t*)rows, stream);
+    TSM_REQUIRE(launch_down((const bf16_t*)act, (const bf16_t*)w2, topk_w, sorted_ids,
+                            expert_ids, total, numel, H, I, E, block_m, weight_layout != 0,
+                            (bf16_t*)rows, stream),
+                TSM_E_SHAPE, "no %d-row down kernel for H=%d I=%d", block_m, H, I);
     return check_launch("down GEMM");
 }
 

@@ -545,6 +545,10 @@ void launch_tile(GemmArgs g, hipStream_t stream) {
 }  // namespace
 
 // Packed weights only; K % 64 == 0; gate_up: 2N % 256 == 0; down: N % 256 == 0.
+bool tile_kernels_take(int H, int I) {
+    return H % 64 == 0 && (2 * I) % kBN == 0 && I % 64 == 0 && H % kBN == 0;
+}
+
 bool launch_tile_gate_up(GemmArgs g, int block_m, hipStream_t stream) {
     if (g.K % 64 != 0 || (2 * g.N) % kBN != 0) return false;
     g.n_tiles = 2 * g.N / kBN;
