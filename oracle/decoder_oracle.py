@@ -27,14 +27,18 @@ def rope_table(D, theta, n):
     return freqs.cos().float(), freqs.sin().float()
 
 
-def decoder_reference(sd, cfg, ids):
-    """sd: parameter name -> CPU tensor (bf16); ids [B, S]. Returns logits [B, S, vocab] fp32."""
+def decoder_reference(sd, cfg, ids, return_route_gaps=False):
+    """sd: parameter name -> CPU tensor (bf16); ids [B, S]. Returns logits [B, S, vocab] fp32;
+    with return_route_gaps, also [B, S]: per position, the smallest gap over the layers between
+    the k-th and the (k+1)-th routing probability (a near tie there can route differently under
+    any other summation order, so a comparison should not rely on such positions)."""
     B, S = ids.shape
     H, Hkv, D = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
     eps, k = cfg.rms_norm_eps, cfg.num_experts_per_tok
     cos, sin = rope_table(D, cfg.rope_theta, S)
-    out = []
+    out, gaps = [], []
     for b in range(B):
+        gap = torch.full((S,), float("inf"))
         x = sd["embed.weight"][ids[b]]                      # [S, hidden] bf16
         residual = None
         for L in range(cfg.num_hidden_layers):
@@ -55,8 +59,14 @@ def decoder_reference(sd, cfg, ids):
             h = rms_norm_ref(residual, sd[p + "post_attn_norm"], eps)
             logits = F.linear(h.float(), sd[p + "mlp.gate.weight"].float())
             w, e = route_torch(logits, k, cfg.norm_topk_prob)
+            srt = logits.softmax(-1).sort(-1, descending=True).values
+            if k < srt.shape[-1]:
+                gap = torch.minimum(gap, srt[:, k - 1] - srt[:, k])
             x = moe_reference(h, sd[p + "mlp.w13"], sd[p + "mlp.w2"], w, e)
         residual = residual + x
         h = rms_norm_ref(residual, sd["norm"], eps)
         out.append((h @ sd["lm_head.weight"].t()).float())
+        gaps.append(gap)
+    if return_route_gaps:
+        return torch.stack(out), torch.stack(gaps)
     return torch.stack(out)

@@ -12,16 +12,35 @@ def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU")
 
 
+def pytest_addoption(parser):
+    parser.addoption("--emulate", action="store_true",
+                     help="run the -m gpu tests on the CPU build of the kernels (tests/emu): a "
+                          "pre-flight check of kernels and tests at small sizes, not GPU parity")
+
+
 @pytest.fixture(scope="session")
-def dev():
+def _emulation(request):
+    if not request.config.getoption("--emulate"):
+        yield False
+        return
+    sys.path.insert(0, os.path.join(ROOT, "tests", "emu"))
+    import harness
+    with harness.emulated(asan=os.environ.get("TSM_EMU_ASAN") == "1"):
+        yield True
+
+
+@pytest.fixture(scope="session")
+def dev(_emulation):
     import torch
+    if _emulation:
+        return torch.device("cpu")
     if not torch.cuda.is_available():
         pytest.skip("no GPU")
     return torch.device("cuda:0")
 
 
 @pytest.fixture(scope="session")
-def tsm():
+def tsm(_emulation):
     import tinyserve_amd
     return tinyserve_amd
 

@@ -52,6 +52,7 @@ def emulated(asan: bool = False):
     patch(attention, "_gpu", no_check)
     patch(ops, "stream_of", no_stream)
     patch(attention, "stream_of", no_stream)
+    patch(L, "stream_of", no_stream)
     import torch
     patch(torch.cuda, "synchronize", lambda *a, **k: None)
     try:

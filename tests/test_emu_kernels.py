@@ -224,9 +224,10 @@ def test_end_to_end_driver(tsm):
     model = build_model(small_cfg(), device="cpu", seed=3, router_logits="fp32")
     prompts = torch.randint(0, 1000, (2, 20), generator=torch.Generator().manual_seed(7))
     toks, _, _ = generate(model, prompts, 4, graph=False)
-    steps = reference_logits(model, torch.cat([prompts, toks[:, :-1]], 1))[:, 19:]
+    ref, gaps = reference_logits(model, torch.cat([prompts, toks[:, :-1]], 1), True)
+    steps = ref[:, 19:]
     top2 = steps.topk(2, dim=-1).values
-    clear = (top2[..., 0] - top2[..., 1]) > 3e-2 * steps.abs().max()
+    clear = ((top2[..., 0] - top2[..., 1]) > 3e-2 * steps.abs().max()) & (gaps[:, 19:] > 2e-3)
     assert bool((toks == steps.argmax(-1))[clear].all())
 
 

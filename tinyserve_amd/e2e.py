@@ -179,7 +179,8 @@ def generate(model, prompts, new_tokens, graph=True, page=16, prefill_chunk=None
     """Greedy generation for a batch of equal-length prompts [B, P]. Returns (tokens [B, N],
     prefill seconds, decode seconds). Prompts are prefilled packed, `prefill_chunk` sequences at a
     time (all by default); each decode step (one token per sequence) is captured once as a HIP
-    graph and replayed (graph=True), as serve.py replays captured decode steps, or run eagerly."""
+    graph and replayed (graph=True, on a GPU), as serve.py replays captured decode steps, or run
+    eagerly."""
     B, P = prompts.shape
     dev = prompts.device
     batch = PagedBatch(B, P + new_tokens, page, dev)
@@ -219,7 +220,7 @@ def generate(model, prompts, new_tokens, graph=True, page=16, prefill_chunk=None
         pos.add_(1)
         col.add_(1)
 
-    if graph and new_tokens > 1:
+    if graph and new_tokens > 1 and prompts.is_cuda:
         # warm up on a side stream (kernels, allocator), then capture one step; the warm-up
         # advanced the state, so rewind it before replaying
         side = torch.cuda.Stream()
