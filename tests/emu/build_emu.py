@@ -31,6 +31,7 @@ ASM_REWRITES = [
     (re.compile(r'asm volatile\("s_waitcnt lgkmcnt\(0\)\\n\\ts_barrier" ::: "memory"\);'),
      "::emu::syncthreads();"),
 ]
+FLAGS = ["-std=c++17", "-O2", "-g", "-fPIC", "-fno-omit-frame-pointer", "-w", "-mavx2", "-mfma"]
 LDS_DECL = re.compile(r"extern __shared__[^;]*\bchar (\w+)\[\];")
 
 
@@ -64,6 +65,7 @@ def build(asan: bool = False, jobs: int = 8) -> str:
         os.path.join(ROOT, "include", "tinyserve_moe.h"), os.path.abspath(__file__)]
     for p in sorted(inputs):
         h.update(open(p, "rb").read())
+    h.update((" ".join(FLAGS) + tag).encode())
     stamp = lib + ".sha256"
     if os.path.exists(lib) and os.path.exists(stamp) and open(stamp).read() == h.hexdigest():
         return lib
@@ -71,11 +73,12 @@ def build(asan: bool = False, jobs: int = 8) -> str:
     obj_dir = os.path.join(OUT, f"obj{tag}")
     os.makedirs(src_dir, exist_ok=True)
     os.makedirs(obj_dir, exist_ok=True)
-    flags = ["-std=c++17", "-O1", "-g", "-fPIC", "-fno-omit-frame-pointer", "-w",
-             f"-I{os.path.join(HERE, 'include')}", f"-I{os.path.join(ROOT, 'include')}",
-             f"-I{CSRC}", "-include", os.path.join(HERE, "emu_hip.h")]
+    flags = FLAGS + [f"-I{os.path.join(HERE, 'include')}", f"-I{os.path.join(ROOT, 'include')}",
+                     f"-I{CSRC}", "-include", os.path.join(HERE, "emu_hip.h")]
     if asan:
-        flags += ["-fsanitize=address,undefined", "-fno-sanitize-recover=undefined"]
+        # -O1: the sanitizer instrumentation at -O2 takes tens of minutes on the router unit
+        flags = [f for f in flags if f != "-O2"] + [
+            "-O1", "-fsanitize=address,undefined", "-fno-sanitize-recover=undefined"]
     units = []
     for f in sources():
         dst = os.path.join(src_dir, f[:-4] + ".cpp")

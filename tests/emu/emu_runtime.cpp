@@ -233,26 +233,26 @@ void complete_wave(int w) {
     }
     if (op.kind == MFMA) {
         if (mask != ~0ull) fail("MFMA with inactive lanes");
-        // A[m][k]: lane m % 16 + 16 * (k / 8), element k % 8; B[k][n] likewise; D[m][n]: lane
-        // n + 16 * (m / 4), element m % 4
-        double A[16][32], B[32][16];
+        // A[m][k]: lane m % 16 + 16 * (k / 8), element k % 8; B[k][n] likewise (kept as
+        // Bt[n][k]); D[m][n]: lane n + 16 * (m / 4), element m % 4. fp32 products and sums.
+        alignas(32) float A[16][32], Bt[16][32];
         for (int l = 0; l < 64; ++l) {
             const Fiber& f = S.fibers[w * 64 + l];
             const uint16_t* a = reinterpret_cast<const uint16_t*>(&f.in[0]);
             const uint16_t* b = reinterpret_cast<const uint16_t*>(&f.in[4]);
             for (int i = 0; i < 8; ++i) {
-                uint32_t av = (uint32_t)a[i] << 16, bv = (uint32_t)b[i] << 16;
-                A[l % 16][8 * (l / 16) + i] = __builtin_bit_cast(float, av);
-                B[8 * (l / 16) + i][l % 16] = __builtin_bit_cast(float, bv);
+                A[l % 16][8 * (l / 16) + i] = __builtin_bit_cast(float, (uint32_t)a[i] << 16);
+                Bt[l % 16][8 * (l / 16) + i] = __builtin_bit_cast(float, (uint32_t)b[i] << 16);
             }
         }
         for (int l = 0; l < 64; ++l) {
             Fiber& f = S.fibers[w * 64 + l];
+            const int n = l % 16;
             for (int i = 0; i < 4; ++i) {
-                const int m = 4 * (l / 16) + i, n = l % 16;
-                double acc = __builtin_bit_cast(float, f.in[8 + i]);
-                for (int k = 0; k < 32; ++k) acc += A[m][k] * B[k][n];
-                f.out[i] = __builtin_bit_cast(uint32_t, (float)acc);
+                const int m = 4 * (l / 16) + i;
+                float acc = 0.0f;
+                for (int k = 0; k < 32; ++k) acc += A[m][k] * Bt[n][k];
+                f.out[i] = __builtin_bit_cast(uint32_t, acc + __builtin_bit_cast(float, f.in[8 + i]));
             }
         }
     }

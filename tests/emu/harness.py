@@ -90,7 +90,8 @@ def run_under_asan(test_file: str, timeout: int = 900, select: str = None):
     preloaded and TSM_EMU_ASAN=1 (the tests then use the ASan build). Returns the
     CompletedProcess."""
     rt = asan_runtime()
-    env = dict(os.environ, TSM_EMU_ASAN="1", LD_PRELOAD=rt or "",
+    preload = " ".join(x for x in (rt, os.environ.get("LD_PRELOAD", "")) if x)
+    env = dict(os.environ, TSM_EMU_ASAN="1", LD_PRELOAD=preload,
                ASAN_OPTIONS="detect_leaks=0:halt_on_error=1:abort_on_error=1",
                UBSAN_OPTIONS="halt_on_error=1:print_stacktrace=1")
     cmd = [sys.executable, "-m", "pytest", "-x", "-q", "-p", "no:cacheprovider", test_file]
