@@ -108,7 +108,8 @@ int tsm_silu_and_mul(const void* gate, int64_t gate_stride, const void* up, int6
  * layout (TSM_LAYOUT_*). The reference picks 16 when T*k <= 4E, else 64 (tinykernels.py:1779);
  * this build picks from its own kernel table: 0 = the expert-major stages below (no tiles, no
  * permutation; T*k <= 12E within their size limits), else 16 (T*k <= 4E) / 64, and 128 for
- * packed weights above 32E.
+ * packed weights above 32E. 256 (packed weights) is returned only where tsm_moe_set_block_m
+ * installed it.
  */
 int tsm_moe_block_m(int64_t T, int H, int I, int E, int top_k, int weight_layout);
 
@@ -117,7 +118,7 @@ int tsm_moe_block_m(int64_t T, int H, int I, int E, int top_k, int weight_layout
  * for assignment counts numel = T * top_k in the power-of-two buckets that [numel_lo, numel_hi]
  * touches (bucket b: 2^b <= numel < 2^(b+1)); block_m = -1 restores the static table there.
  * 0 selects the expert-major stages (used only where their size limits allow), 16 / 64 (and 128
- * with packed weights) the tiled stages. Process-wide; plans already captured in a HIP graph keep
+ * or 256 with packed weights, where 2I and H are multiples of 256) the tiled stages. Process-wide; plans already captured in a HIP graph keep
  * their kernels. Workspace sizes follow the installed heights, so query them after installing.
  * The build's counterpart of the autotuning of autotune_fused_moe (tinykernels.py:1798-1811):
  * kernels.autotune_fused_moe times the candidates and installs the fastest.
@@ -141,7 +142,7 @@ int tsm_fused_moe(const void* x, const void* w13, const void* w2, const float* t
  * The stages of tsm_fused_moe, for callers that schedule them separately (and for per-kernel
  * timing). Each is one launch of the corresponding stage of _moe_gemm / _fused_moe_kernel
  * (tinykernels.py:1746-1765, 1589-1744) on the outputs of tsm_moe_align for the same block_m
- * (supported: 16, 64; 128 with packed weights):
+ * (supported: 16, 64; 128 and 256 with packed weights):
  *   gate_up: act[max_padded, I] (expert-sorted rows) = bf16(bf16(silu(bf16(x W1^T))) *
  *            bf16(x W3^T)) with x gathered as x[sorted_ids[r] / top_k]; rows of remote tiles
  *            are not written.

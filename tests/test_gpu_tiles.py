@@ -1,7 +1,7 @@
 """The stage entry points (align, gate_up, down, combine) at the pipelined tile heights.
 
-The 64- and 128-row tile kernels accumulate each output over K in one fp32 chain in the same
-order, so their outputs are equal bit for bit; the result also equals the planned
+The 64-, 128- and 256-row tile kernels accumulate each output over K in one fp32 chain in the
+same order, so their outputs are equal bit for bit; the result also equals the planned
 fused_moe_packed at the same batch (a tile-kernel size) and, at a small batch, the oracle within
 the bf16 tolerance."""
 import pytest
@@ -48,13 +48,14 @@ def test_tile_heights_agree(dev, tsm, H, I, E, k, T):
     x, gw, w13, w2 = make_layer(T, H, E, I, torch.bfloat16, seed=T + E, device=dev)
     p13, p2 = tsm.pack_moe_weights(w13, w2)
     w, ids, _ = tsm.moe_router(x, gw, k, True)
-    outs = {bm: staged(tsm, x, p13, p2, w, ids, E, I, bm) for bm in (64, 128)}
+    outs = {bm: staged(tsm, x, p13, p2, w, ids, E, I, bm) for bm in (64, 128, 256)}
     assert torch.equal(outs[64], outs[128]), "64 vs 128"
+    assert torch.equal(outs[128], outs[256]), "128 vs 256"
     fused = tsm.fused_moe_packed(x, p13, p2, w, ids)
     assert torch.equal(fused, outs[128])
 
 
-@pytest.mark.parametrize("bm", [64, 128])
+@pytest.mark.parametrize("bm", [64, 128, 256])
 def test_tile_heights_against_oracle(dev, tsm, bm):
     H, I, E, k, T = 768, 384, 32, 4, 40
     x, gw, w13, w2 = make_layer(T, H, E, I, torch.bfloat16, seed=5, device=dev)

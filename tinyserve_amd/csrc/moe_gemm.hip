@@ -286,7 +286,7 @@ Plan plan_for(int64_t T, int H, int I, int E, int top_k, bool packed) {
         const int o = g_block_m_override[packed][numel_bucket(numel)].load(std::memory_order_relaxed);
         // an installed height applies where its kernels take the shape
         if (o == 0 && expert_path_supported(numel, H, I, E)) return Plan{0};
-        if (o > 0 && block_m_supported(o, packed) && (o != 128 || tile_kernels_take(H, I)))
+        if (o > 0 && block_m_supported(o, packed) && (o < 128 || tile_kernels_take(H, I)))
             return Plan{o};
     }
     if (numel >= 1 && numel <= 12ll * E && expert_path_supported(numel, H, I, E))
@@ -372,7 +372,9 @@ GemmArgs gemm_args(const bf16_t* A, const bf16_t* B, bf16_t* C, const float* top
 
 bool block_m_supported(int block_m, bool packed) {
     if (block_m == 0) return false;  // the expert-major path has its own entry points
-    return block_m == 16 || block_m == 64 || (packed && block_m == 128);
+    // 128 and 256 rows: the pipelined tile kernels, packed weights only (256 is never chosen by
+    // the static table; it is installed by autotuning where it measures faster)
+    return block_m == 16 || block_m == 64 || (packed && (block_m == 128 || block_m == 256));
 }
 
 // gate_up GEMM + SwiGLU: act[max_padded, I] from x[T, H] and w13[E, 2I, H].
@@ -387,8 +389,8 @@ void launch_lds(const GemmArgs& g, bool packed, hipStream_t stream) {
                            stream, g);
 }
 
-// false: no kernel for this tile height and shape (nothing launched). 128-row tiles have only the
-// pipelined tile kernel; 16 and 64 fall back to the LDS kernel of their own height.
+// false: no kernel for this tile height and shape (nothing launched). 128- and 256-row tiles have
+// only the pipelined tile kernel; 16 and 64 fall back to the LDS kernel of their own height.
 bool launch_gate_up(const bf16_t* x, const bf16_t* w13, const int32_t* sorted,
                     const int32_t* eids, const int32_t* total, int64_t numel, int top_k, int H,
                     int I, int E, int block_m, bool packed, bf16_t* act, hipStream_t stream) {

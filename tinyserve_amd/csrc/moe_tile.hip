@@ -1,8 +1,11 @@
-// LDS-pipelined grouped GEMMs for prefill-sized batches (64/128-row expert tiles).
+// LDS-pipelined grouped GEMMs for prefill-sized batches (64/128/256-row expert tiles).
 //
 // Workgroup tile: BM expert-sorted rows x 256 rows of B (gate_up: 8 gate + 8 up 16-row blocks ->
-// 128 activation columns; down: 256 output columns), 8 wavefronts in a (BM/64) x (512/BM) grid,
-// each owning a 64-row block of C in 16x16x32 bf16 MFMA accumulators.
+// 128 activation columns; down: 256 output columns), 8 wavefronts in a WM x (8/WM) grid (WM = 1
+// for 64 rows, 2 for 128 and 256), each owning a (BM/WM) x (256*WM/8) block of C in 16x16x32
+// bf16 MFMA accumulators. A 256-row tile reads each weight panel once for both 128-row halves
+// of an expert's rows (a half of padding rows only is skipped), at the cost of streaming its A
+// fragments in halves to fit the accumulators in the register budget.
 //
 // Operands reach LDS through direct global->LDS loads (global_load_lds_dwordx4: 64 lanes x 16 B,
 // written to LDS at lane*16), in stages of 64 k through a ring of NS stages:
@@ -312,7 +315,28 @@ __global__ __launch_bounds__(64 * kNW, 1) void moe_tile_kernel(GemmArgs p) {
         return __builtin_amdgcn_readlane(k < 64 ? remap0 : remap1, k & 63);
     };
 
+    // the halves of the A fragments (f = h * FM/2 + i) and the B fragments of one k-step
+    auto read_a_half = [&](int st, int kk, int h, u32x4 (&af)[FM / 2]) {
+        const uint32_t ab = lds0 + (st & 1) * A_BYTES + a_off[kk];
+#pragma unroll
+        for (int i = 0; i < FM / 2; ++i)
+            af[i] = lds_read16(ab + (wm * FM + h * (FM / 2) + i) * 2 * kBlk);
+    };
+    auto read_b = [&](int st, int kk, u32x4 (&bfr)[FN]) {
+        const uint32_t bb = lds0 + 2 * A_BYTES + (st % NB) * B_BYTES + kk * kBlk + lane * 16;
+#pragma unroll
+        for (int g = 0; g < FN; ++g) bfr[g] = lds_read16(bb + (wn * FN + g) * 2 * kBlk);
+    };
+
     f32x4 acc[FM][FN];
+    auto mfma_half = [&](int h, const u32x4 (&af)[FM / 2], const u32x4 (&bfr)[FN]) {
+#pragma unroll
+        for (int i = 0; i < FM / 2; ++i)
+#pragma unroll
+            for (int g = 0; g < FN; ++g)
+                acc[h * (FM / 2) + i][g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                    as_bf16x8(af[i]), as_bf16x8(bfr[g]), acc[h * (FM / 2) + i][g], 0, 0, 0);
+    };
     auto mfmas = [&](const u32x4 (&af)[FM], const u32x4 (&bfr)[FN]) {
 #pragma unroll
         for (int f = 0; f < FM; ++f)
@@ -385,7 +409,37 @@ __global__ __launch_bounds__(64 * kNW, 1) void moe_tile_kernel(GemmArgs p) {
         if (next < chunk_end) fetch(tile_index(next));
         if (1 < NST) issue_a(1);
         if (LB < NST) issue_b(LB);
-        if (active) {
+        if (!active) {
+            for (int st = 0; st + 1 < NST; ++st) advance(st);
+        } else if constexpr (FM >= 8) {
+            // 256-row tiles (a 128 x 64 block per wavefront): the accumulators take half of the
+            // register budget, so A is streamed in halves of FM/2 fragments instead of being
+            // double-buffered whole: the first half's MFMAs run while the second half is read,
+            // the second half's while the next k-step's first half and B are read. The two B
+            // sets alternate roles between k-steps, so a stage ends with the next one's first
+            // B set in bc.
+            constexpr int FH = FM / 2;
+            u32x4 aL[FH], aH[FH], bc[FN], bn[FN];
+            read_a_half(0, 0, 0, aL);
+            read_b(0, 0, bc);
+            for (int st = 0; st < NST; ++st) {
+                read_a_half(st, 0, 1, aH);
+                mfma_half(0, aL, bc);
+                interleave_reads_mfma<FH, FH * FN>();
+                read_a_half(st, 1, 0, aL);
+                read_b(st, 1, bn);
+                mfma_half(1, aH, bc);
+                interleave_reads_mfma<FH + FN, FH * FN>();
+                read_a_half(st, 1, 1, aH);
+                mfma_half(0, aL, bn);
+                interleave_reads_mfma<FH, FH * FN>();
+                if (st + 1 < NST) advance(st);
+                read_a_half(st + 1, 0, 0, aL);
+                read_b(st + 1, 0, bc);
+                mfma_half(1, aH, bn);
+                interleave_reads_mfma<FH + FN, FH * FN>();
+            }
+        } else {
             u32x4 a0[FM], b0[FN], a1[FM], b1[FN];
             read_frags(0, 0, a0, b0);
             // One straight-line body per stage (no path split around the last stage) keeps the
@@ -400,8 +454,6 @@ __global__ __launch_bounds__(64 * kNW, 1) void moe_tile_kernel(GemmArgs p) {
                 mfmas(a1, b1);
                 interleave_reads_mfma<NR, NM>();
             }
-        } else {
-            for (int st = 0; st + 1 < NST; ++st) advance(st);
         }
 
         if (!GATEUP) row_w = settle(cur_flat < p.numel ? row_w : 0.0f);
@@ -552,7 +604,8 @@ bool tile_kernels_take(int H, int I) {
 bool launch_tile_gate_up(GemmArgs g, int block_m, hipStream_t stream) {
     if (g.K % 64 != 0 || (2 * g.N) % kBN != 0) return false;
     g.n_tiles = 2 * g.N / kBN;
-    if (block_m == 128) launch_tile<128, true>(g, stream);
+    if (block_m == 256) launch_tile<256, true>(g, stream);
+    else if (block_m == 128) launch_tile<128, true>(g, stream);
     else if (block_m == 64) launch_tile<64, true>(g, stream);
     else return false;
     return true;
@@ -561,7 +614,8 @@ bool launch_tile_gate_up(GemmArgs g, int block_m, hipStream_t stream) {
 bool launch_tile_down(GemmArgs g, int block_m, hipStream_t stream) {
     if (g.K % 64 != 0 || g.N % kBN != 0) return false;
     g.n_tiles = g.N / kBN;
-    if (block_m == 128) launch_tile<128, false>(g, stream);
+    if (block_m == 256) launch_tile<256, false>(g, stream);
+    else if (block_m == 128) launch_tile<128, false>(g, stream);
     else if (block_m == 64) launch_tile<64, false>(g, stream);
     else return false;
     return true;

@@ -10,8 +10,9 @@ the gfx950 HIP kernels. `SparseMoE.forward` (serve.py:1076-1087) calls these thr
     autotune_fused_moe(w13, w2, top_k, max_num_tokens)         tinykernels.py:1799
 
 autotune_fused_moe times the kernel families and tile heights this build has (expert-major,
-16-, 64- and, with packed weights, 128-row tiles) per power-of-two bucket of assignment counts and
-installs the fastest in the library's plan table (set_moe_block_m).
+16-, 64- and, with packed weights, 128- and 256-row tiles) per power-of-two bucket of assignment
+counts and installs the fastest in the library's plan table (set_moe_block_m). 256-row tiles
+exist only through it: the static table never picks them.
 """
 import torch
 
@@ -58,6 +59,8 @@ def set_moe_block_m(numel_lo: int, numel_hi: int, block_m: int, packed: bool = F
 
 def _candidates(numel: int, E: int, packed: bool):
     c = [16, 64] + ([128] if packed else [])
+    if packed and numel > 32 * E:   # 256-row tiles: only where experts average > 32 rows
+        c.append(256)
     if numel <= 4096:   # the expert-major stages' row limit
         c.insert(0, 0)
     return c
