@@ -10,12 +10,35 @@ if ROOT not in sys.path:
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU")
+    config.addinivalue_line("markers", "emu_tokens(n): a GPU test whose batch is n tokens (for "
+                                       "--emulate-max-tokens when the size is not a T parameter)")
+    config.addinivalue_line("markers", "emu_skip(reason): a GPU test the CPU emulation cannot run")
 
 
 def pytest_addoption(parser):
     parser.addoption("--emulate", action="store_true",
                      help="run the -m gpu tests on the CPU build of the kernels (tests/emu): a "
                           "pre-flight check of kernels and tests at small sizes, not GPU parity")
+    parser.addoption("--emulate-max-tokens", type=int, default=1024,
+                     help="with --emulate, skip cases of more tokens than this (a Qwen3-30B "
+                          "layer of 512 tokens takes about 80 s on the emulation)")
+
+
+def pytest_collection_modifyitems(config, items):
+    if not config.getoption("--emulate"):
+        return
+    limit = config.getoption("--emulate-max-tokens")
+    for item in items:
+        why = item.get_closest_marker("emu_skip")
+        if why is not None:
+            item.add_marker(pytest.mark.skip(reason=f"not on the CPU emulation: {why.args[0]}"))
+            continue
+        mark = item.get_closest_marker("emu_tokens")
+        callspec = getattr(item, "callspec", None)
+        T = mark.args[0] if mark else (callspec.params.get("T") if callspec else None)
+        if isinstance(T, int) and T > limit:
+            item.add_marker(pytest.mark.skip(
+                reason=f"{T} tokens: above --emulate-max-tokens={limit}"))
 
 
 @pytest.fixture(scope="session")
@@ -25,7 +48,7 @@ def _emulation(request):
         return
     sys.path.insert(0, os.path.join(ROOT, "tests", "emu"))
     import harness
-    with harness.emulated(asan=os.environ.get("TSM_EMU_ASAN") == "1"):
+    with harness.emulated(harness.sanitizer_from_env()):
         yield True
 
 

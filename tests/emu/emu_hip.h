@@ -44,7 +44,10 @@ const Index& grid_dim();
 int lane();
 void launch(dim3 grid, dim3 block, size_t dyn_lds, std::function<void()> body);
 char* dynamic_lds();
+void* static_lds(int key, size_t bytes, size_t align);
 void syncthreads();
+void s_barrier();
+void s_waitcnt(int imm);
 void wave_barrier();
 uint32_t shfl_u32(uint32_t v, int src_lane_xor, int mode, int width);
 uint64_t ballot(bool p);
@@ -113,7 +116,10 @@ inline int __popcll(unsigned long long v) { return __builtin_popcountll(v); }
 inline int __popc(unsigned v) { return __builtin_popcount(v); }
 inline int __ffsll(unsigned long long v) { return __builtin_ffsll((long long)v); }
 inline int __clzll(unsigned long long v) { return v ? __builtin_clzll(v) : 64; }
-template <typename T> inline T atomicAdd(T* p, T v) { T o = *p; *p = o + v; return o; }
+template <typename T> inline T atomicAdd(T* p, T v) {
+    static_assert(sizeof(T) == 4 || sizeof(T) == 8, "32/64-bit atomics");
+    return __atomic_fetch_add(p, v, __ATOMIC_RELAXED);   // relaxed, as the device's atomics
+}
 inline float __expf(float x) { return expf(x); }
 inline float __uint_as_float(uint32_t v) { return __builtin_bit_cast(float, v); }
 inline uint32_t __float_as_uint(float v) { return __builtin_bit_cast(uint32_t, v); }
@@ -130,7 +136,7 @@ inline int64_t min(int a, int64_t b) { return a < b ? a : b; }
 inline uint64_t min(uint64_t a, uint64_t b) { return a < b ? a : b; }
 
 // AMDGPU builtins
-#define __builtin_amdgcn_s_waitcnt(x) ((void)0)
+#define __builtin_amdgcn_s_waitcnt(x) ::emu::s_waitcnt(x)
 #define __builtin_amdgcn_sched_barrier(x) ((void)0)
 #define __builtin_amdgcn_sched_group_barrier(a, b, c) ((void)0)
 #define __builtin_amdgcn_fence(order, scope) ((void)0)

@@ -6,7 +6,30 @@
 // workgroup or wavefront). The last one to arrive evaluates the operation for all of them. A
 // wavefront whose lanes reach different cross-lane operations, or a barrier that some threads
 // never reach, is reported as an error (it is undefined on the GPU).
+//
+// Global->LDS loads are asynchronous, as on the GPU: each lane queues its copies in issue order
+// and they land in the LDS only when the wavefront waits for them (s_waitcnt with a vmcnt bound,
+// a wave rendezvous that lands all but the newest N of every lane's copies), when the thread
+// reaches __syncthreads() (whose release fence drains the counters), or when it exits. A plain
+// s_barrier does not land them. A kernel that reads a stage of its LDS ring before waiting for
+// it therefore reads what the slot held before, and its results are wrong on the CPU as well.
+//
+// LDS, static (__shared__ declarations, turned into references into an arena by the build) and
+// dynamic, is refilled with a garbage pattern at the start of every workgroup.
+//
+// With EMU_TSAN (the ThreadSanitizer build; the kernels instrumented, this file not), every
+// wavefront is one ThreadSanitizer fiber (its lanes run in lockstep on the GPU, so they are one
+// thread of program order here, in the emulator's execution order; one fiber per lane would also
+// exceed the sanitizer's slot count at 256-thread workgroups, which makes it drop its history),
+// created afresh for each workgroup with fresh stacks, and the only happens-before edges are
+// those the GPU provides: the launch before each wavefront; a workgroup barrier (arrivals before
+// departures, per barrier generation); every wavefront before the end of the launch as the host
+// sees it. Accesses of two workgroups of one launch,
+// or of two wavefronts between barriers, that touch the same bytes with one of them a write
+// and not both atomic are then reported as data races.
 #include <sys/mman.h>
+
+#include <unordered_map>
 
 #include <cstdio>
 #include <cstdlib>
@@ -42,14 +65,45 @@ emu_swap:
     .size emu_swap, .-emu_swap
 )");
 
+#ifdef EMU_TSAN
+extern "C" {
+void* __tsan_get_current_fiber(void);
+void* __tsan_create_fiber(unsigned flags);
+void __tsan_destroy_fiber(void* fiber);
+void __tsan_switch_to_fiber(void* fiber, unsigned flags);
+void __tsan_acquire(void* addr);
+void __tsan_release(void* addr);
+void __tsan_read_range(void* addr, unsigned long size);
+void __tsan_write_range(void* addr, unsigned long size);
+void AnnotateIgnoreWritesBegin(const char* file, int line);
+void AnnotateIgnoreWritesEnd(const char* file, int line);
+}
+#define TSAN(...) __VA_ARGS__
+#else
+#define TSAN(...)
+#endif
+
 namespace emu {
 namespace {
 
+#ifdef EMU_TSAN
+constexpr size_t kStack = 128 << 10;     // per fiber, remapped for every workgroup
+#else
 constexpr size_t kStack = 1 << 20;       // per fiber (reserved lazily by the kernel)
+#endif
 constexpr size_t kLds = 160 * 1024;      // dynamic LDS of one workgroup
+constexpr size_t kArena = 4 << 20;       // static LDS declarations of every kernel
 constexpr int kMaxIn = 12;               // 32-bit words of a lane's operand (MFMA: a, b, c)
 
-enum Kind { NONE = 0, SHFL, BALLOT, READLANE, READFIRST, DPP, MFMA, WBAR };
+enum Kind { NONE = 0, SHFL, BALLOT, READLANE, READFIRST, DPP, MFMA, WBAR, VMWAIT };
+
+constexpr int kMaxVm = 63;               // the vmcnt counter's range (issue stalls beyond it)
+
+struct AsyncCopy {
+    const void* src;
+    uintptr_t dst;
+    int size;
+};
 
 struct Fiber {
     void* sp = nullptr;
@@ -63,7 +117,22 @@ struct Fiber {
     bool pred = false;
     bool pending = false;      // waiting in a wave operation
     bool at_barrier = false;   // waiting in a workgroup barrier
+    AsyncCopy q[kMaxVm];       // global->LDS copies in flight, oldest first (ring)
+    int q_head = 0, q_len = 0;
+    int bar_gen = 0;           // barrier generation this thread waits in
 };
+
+// Lands the oldest copies of `f` until at most `keep` remain.
+void land_copies(Fiber& f, int keep) {
+    while (f.q_len > keep) {
+        const AsyncCopy& c = f.q[f.q_head];
+        TSAN(__tsan_read_range(const_cast<void*>(c.src), c.size);
+             __tsan_write_range(reinterpret_cast<void*>(c.dst), c.size);)
+        memcpy(reinterpret_cast<void*>(c.dst), c.src, c.size);
+        f.q_head = (f.q_head + 1) % kMaxVm;
+        f.q_len--;
+    }
+}
 
 struct WaveOp {
     Kind kind = NONE;
@@ -78,6 +147,14 @@ struct State {
     std::vector<WaveOp> waves;
     int nthreads = 0;
     int bar_arrived = 0;
+    int bar_gen = 0;
+    char* arena = nullptr;               // static LDS (below 4 GiB, like the dynamic LDS)
+    size_t arena_used = 0;
+    std::unordered_map<uint64_t, size_t> arena_at;   // (declaration, size) -> offset
+    void* tsan_main = nullptr;
+    char* tokens = nullptr;              // this workgroup's synchronisation addresses
+    char* end_token = nullptr;           // the launch's: every thread -> the host
+    std::vector<void*> wave_tsan;        // ThreadSanitizer fiber per wavefront (EMU_TSAN)
     Index bidx{0, 0, 0}, bdim{1, 1, 1}, gdim{1, 1, 1};
     Fiber* cur = nullptr;
     void* sched_sp = nullptr;
@@ -88,6 +165,11 @@ struct State {
 
 State S;
 
+// Synchronisation addresses of the current workgroup (EMU_TSAN), fresh for each workgroup so
+// that no edge leads from one workgroup to another: [0] launch, [2..3] barrier generations
+// ([1] unused; the end of the launch has its own address).
+void* token(int i) { return S.tokens + i; }
+
 [[noreturn]] void fail(const std::string& m) {
     fprintf(stderr, "emu: %s (block %u,%u,%u thread %d)\n", m.c_str(), S.bidx.x, S.bidx.y,
             S.bidx.z, S.cur ? S.cur->tid : -1);
@@ -95,13 +177,15 @@ State S;
     abort();
 }
 
+char* map_low(size_t bytes) {
+    void* p = mmap(nullptr, bytes, PROT_READ | PROT_WRITE, MAP_PRIVATE | MAP_ANONYMOUS | MAP_32BIT,
+                   -1, 0);
+    if (p == MAP_FAILED) fail("cannot map LDS below 4 GiB");
+    return static_cast<char*>(p);
+}
+
 char* low_lds() {
-    if (!S.lds) {
-        void* p = mmap(nullptr, kLds, PROT_READ | PROT_WRITE,
-                       MAP_PRIVATE | MAP_ANONYMOUS | MAP_32BIT, -1, 0);
-        if (p == MAP_FAILED) fail("cannot map LDS below 4 GiB");
-        S.lds = static_cast<char*>(p);
-    }
+    if (!S.lds) S.lds = map_low(kLds);
     return S.lds;
 }
 
@@ -109,20 +193,29 @@ void try_complete_wave(int w);
 void try_complete_barrier();
 int wave_of(const Fiber* f) { return f->tid / 64; }
 
-void yield_blocked() {
-    Fiber* f = S.cur;
-    f->runnable = false;
+// Switches from the running thread to the scheduler.
+void to_scheduler(Fiber* f) {
+    TSAN(__tsan_switch_to_fiber(S.tsan_main, 1);)
     emu_swap(&f->sp, S.sched_sp);
 }
 
+void yield_blocked() {
+    Fiber* f = S.cur;
+    f->runnable = false;
+    to_scheduler(f);
+}
+
 void fiber_entry() {
+    TSAN(__tsan_acquire(token(0));)
     (*S.body)();
     Fiber* f = S.cur;
+    land_copies(*f, 0);   // loads still in flight at the end of the program land regardless
+    TSAN(__tsan_release(S.end_token);)
     f->done = true;
     // a finished thread no longer takes part in its workgroup's barrier or its wave's ops
     try_complete_wave(wave_of(f));
     try_complete_barrier();
-    emu_swap(&f->sp, S.sched_sp);
+    to_scheduler(f);
     fail("finished fiber resumed");
 }
 
@@ -149,6 +242,7 @@ void try_complete_barrier() {
     for (int t = 0; t < S.nthreads; ++t) live += !S.fibers[t].done;
     if (S.bar_arrived > 0 && S.bar_arrived == live) {
         S.bar_arrived = 0;
+        S.bar_gen++;
         for (int t = 0; t < S.nthreads; ++t)
             if (!S.fibers[t].done) {
                 S.fibers[t].at_barrier = false;
@@ -224,6 +318,9 @@ void complete_wave(int w) {
                 f.out[0] = valid ? lane_in(w, s, 1) : (op.p3 ? 0u : f.in[0]);
                 break;
             }
+            case VMWAIT:
+                land_copies(f, op.p0);
+                break;
             case MFMA:
             case WBAR:
                 break;
@@ -293,18 +390,53 @@ const Index& block_dim() { return S.bdim; }
 const Index& grid_dim() { return S.gdim; }
 int lane() { return S.cur->tid & 63; }
 char* dynamic_lds() { return low_lds(); }
+
+void* static_lds(int key, size_t bytes, size_t align) {
+    const uint64_t k = (uint64_t)key << 40 | bytes;
+    auto it = S.arena_at.find(k);
+    if (it == S.arena_at.end()) {
+        const size_t a = align < 16 ? 16 : align;
+        const size_t off = (S.arena_used + a - 1) / a * a;
+        if (off + bytes > kArena) fail("static LDS arena exhausted");
+        S.arena_used = off + bytes;
+        // the fill stands for the state the workgroup finds, not for an access of this thread
+        TSAN(AnnotateIgnoreWritesBegin(__FILE__, __LINE__);)
+        memset(S.arena + off, 0xFF, bytes);
+        TSAN(AnnotateIgnoreWritesEnd(__FILE__, __LINE__);)
+        it = S.arena_at.emplace(k, off).first;
+    }
+    return S.arena + it->second;
+}
 hipError_t last_error() {
     const hipError_t e = S.err;
     S.err = hipSuccess;
     return e;
 }
 
-void syncthreads() {
+void barrier_arrive() {
     Fiber* f = S.cur;
+    f->bar_gen = S.bar_gen;
+    TSAN(__tsan_release(token(2 + (f->bar_gen & 1)));)
     S.bar_arrived++;
     f->at_barrier = true;
     try_complete_barrier();
     while (f->at_barrier) yield_blocked();
+    TSAN(__tsan_acquire(token(2 + (f->bar_gen & 1)));)
+}
+
+void syncthreads() {
+    land_copies(*S.cur, 0);   // __syncthreads' release fence waits for the vector counters
+    barrier_arrive();
+}
+
+void s_barrier() { barrier_arrive(); }
+
+void s_waitcnt(int imm) {
+    // gfx9 encoding: vmcnt in bits 3:0 and 15:14; only the vector-memory count is modelled
+    // (LDS and scalar accesses complete at once here)
+    const int vm = (imm & 15) | (((imm >> 14) & 3) << 4);
+    if (vm >= kMaxVm) return;
+    wave_arrive(VMWAIT, vm);
 }
 
 void wave_barrier() { wave_arrive(WBAR); }
@@ -355,7 +487,10 @@ void global_load_lds(const void* g, uintptr_t lds, int size, int offset) {
     const uintptr_t lo = (uintptr_t)low_lds();
     const uintptr_t dst = lds + offset + (uintptr_t)lane() * size;
     if (dst < lo || dst + size > lo + kLds) fail("global_load_lds outside the LDS");
-    memcpy(reinterpret_cast<void*>(dst), g, size);
+    Fiber& f = *S.cur;
+    if (f.q_len == kMaxVm) land_copies(f, kMaxVm - 1);   // the counter is full: issue waits
+    f.q[(f.q_head + f.q_len) % kMaxVm] = AsyncCopy{g, dst, size};
+    f.q_len++;
 }
 
 void launch(dim3 grid, dim3 block, size_t dyn_lds, std::function<void()> body) {
@@ -382,11 +517,38 @@ void launch(dim3 grid, dim3 block, size_t dyn_lds, std::function<void()> body) {
         if (stacks[t] == MAP_FAILED) fail("cannot map a fiber stack");
     }
     low_lds();
+    // mapped here, by the host side: a mapping is an access of the thread that makes it
+    if (!S.arena) S.arena = map_low(kArena);
+#ifdef EMU_TSAN
+    S.tsan_main = __tsan_get_current_fiber();
+    S.end_token = static_cast<char*>(malloc(1));
+    if (!S.end_token) fail("out of memory");
+#endif
     for (unsigned bz = 0; bz < grid.z; ++bz)
         for (unsigned by = 0; by < grid.y; ++by)
             for (unsigned bx = 0; bx < grid.x; ++bx) {
                 S.bidx = Index{bx, by, bz};
+#ifdef EMU_TSAN
+                // this workgroup's memory is new to it: fresh stacks, LDS history forgotten
+                for (int t = 0; t < n; ++t) {
+                    munmap(stacks[t], kStack);
+                    stacks[t] = static_cast<char*>(mmap(nullptr, kStack, PROT_READ | PROT_WRITE,
+                                                        MAP_PRIVATE | MAP_ANONYMOUS | MAP_NORESERVE,
+                                                        -1, 0));
+                    if (stacks[t] == MAP_FAILED) fail("cannot map a fiber stack");
+                }
+                munmap(S.lds, kLds);   // the interceptors forget the old mappings' history
+                S.lds = map_low(kLds);
+                munmap(S.arena, kArena);
+                S.arena = map_low(kArena);
+                S.tokens = static_cast<char*>(malloc(4));
+                if (!S.tokens) fail("out of memory");
+                S.wave_tsan.assign(S.waves.size(), nullptr);
+                for (auto& wf : S.wave_tsan) wf = __tsan_create_fiber(0);
+#endif
                 memset(S.lds, 0xFF, kLds);   // LDS starts as garbage (NaN patterns)
+                memset(S.arena, 0xFF, S.arena_used);
+                S.bar_gen = 0;
                 S.bar_arrived = 0;
                 for (auto& w : S.waves) w = WaveOp{};
                 for (int t = 0; t < n; ++t) {
@@ -401,6 +563,7 @@ void launch(dim3 grid, dim3 block, size_t dyn_lds, std::function<void()> body) {
                     for (int r = 0; r < 6; ++r) *--sp = 0;        // rbp rbx r12-r15
                     f.sp = sp;
                 }
+                TSAN(__tsan_release(token(0));)
                 for (;;) {
                     bool progress = false, all_done = true;
                     for (int t = 0; t < n; ++t) {
@@ -409,6 +572,7 @@ void launch(dim3 grid, dim3 block, size_t dyn_lds, std::function<void()> body) {
                         all_done = false;
                         if (!f.runnable) continue;
                         S.cur = &f;
+                        TSAN(__tsan_switch_to_fiber(S.wave_tsan[t / 64], 1);)
                         emu_swap(&S.sched_sp, f.sp);
                         S.cur = nullptr;
                         progress = true;
@@ -416,8 +580,18 @@ void launch(dim3 grid, dim3 block, size_t dyn_lds, std::function<void()> body) {
                     if (all_done) break;
                     if (!progress) fail("deadlock: a barrier or wave operation never completes");
                 }
+#ifdef EMU_TSAN
+                for (void* wf : S.wave_tsan) __tsan_destroy_fiber(wf);
+                free(S.tokens);             // drops this workgroup's synchronisation state
+                S.tokens = nullptr;
+#endif
             }
     for (int t = 0; t < n; ++t) munmap(stacks[t], kStack);
+#ifdef EMU_TSAN
+    __tsan_acquire(S.end_token);   // the host sees the whole launch complete
+    free(S.end_token);
+    S.end_token = nullptr;
+#endif
     S.body = nullptr;
 }
 

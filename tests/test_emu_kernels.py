@@ -9,8 +9,9 @@ the GPU's own arithmetic (the matrix-core instruction is evaluated in double pre
 anything about timing, memory ordering between workgroups or the compiler's device code
 generation. The -m gpu tests remain the parity tests proper.
 
-The same cases also run under AddressSanitizer (test_emu_asan.py) so that any out-of-bounds
-access of a kernel is caught on the CPU."""
+The same cases also run under AddressSanitizer and ThreadSanitizer (test_emu_sanitizers.py), so
+that an out-of-bounds access, or a data race between wavefronts or workgroups, of a kernel is
+caught on the CPU."""
 import os
 import sys
 
@@ -27,13 +28,10 @@ from oracle import c_oracle  # noqa: E402
 from oracle.moe_oracle import (add_rmsnorm_reference, make_layer,  # noqa: E402
                                moe_align_block_size_np, moe_reference)
 
-ASAN = os.environ.get("TSM_EMU_ASAN") == "1"
-
-
 @pytest.fixture(scope="module")
 def tsm():
     import tinyserve_amd
-    with harness.emulated(asan=ASAN):
+    with harness.emulated(harness.sanitizer_from_env()):
         yield tinyserve_amd
 
 
@@ -91,11 +89,12 @@ def test_align_bitexact(tsm, numel, E, bm):
     assert int(t[0]) == int(rt[0])
 
 
-@pytest.mark.parametrize("T", [2, 40, 300])
-def test_experts_every_plan(tsm, T):
+@pytest.mark.parametrize("T", [2, 40, 300, 700])   # 700: experts past 128 rows (256-row tiles
+def test_experts_every_plan(tsm, T):                # with both halves active)
     """Every plan the static table or the tuner can pick (expert-major, 16-, 64-row tiles;
-    128-row persistent tiles on packed weights), both weight layouts, against the oracle; the
-    packed and reference-layout kernels of a plan agree bit for bit."""
+    128- and 256-row persistent tiles on packed weights), both weight layouts, against the
+    oracle; the packed and reference-layout kernels of a plan agree bit for bit, and so do the
+    64-, 128- and 256-row tile kernels (one fp32 chain per output in the same k order)."""
     from tinyserve_amd import kernels
     H, E, I, k = 256, 8, 512, 2
     x, gw, w13, w2 = make_layer(T, H, E, I, torch.bfloat16, seed=10 + T)
@@ -103,10 +102,11 @@ def test_experts_every_plan(tsm, T):
     ref = moe_reference(x, w13, w2, w, ids.long())
     p13, p2 = tsm.pack_moe_weights(w13, w2)
     numel = T * k
+    tiles = {}
     try:
-        for bm in (0, 16, 64, 128):
+        for bm in (0, 16, 64, 128, 256):
             for packed in (False, True):
-                if bm == 128 and not packed:
+                if bm >= 128 and not packed:
                     continue
                 kernels.set_moe_block_m(numel, numel, bm, packed)
                 if kernels.moe_block_m(T, H, I, E, k, packed) != bm:
@@ -114,12 +114,44 @@ def test_experts_every_plan(tsm, T):
                 out = (tsm.fused_moe_packed(x, p13, p2, w, ids) if packed
                        else tsm.fused_moe(x, w13, w2, w, ids))
                 close(out, ref)
-                if packed and bm != 128:
+                if packed and bm >= 64:
+                    tiles[bm] = out
+                if packed and bm < 128:
                     kernels.set_moe_block_m(numel, numel, bm, False)
                     assert torch.equal(out, tsm.fused_moe(x, w13, w2, w, ids)), bm
+        assert set(tiles) == {64, 128, 256}
+        assert torch.equal(tiles[64], tiles[128]) and torch.equal(tiles[128], tiles[256])
     finally:
         kernels.set_moe_block_m(1, 1 << 30, -1, False)
         kernels.set_moe_block_m(1, 1 << 30, -1, True)
+
+
+@pytest.mark.parametrize("packed", [False, True])
+def test_autotune_small_layer(tsm, packed):
+    """autotune_fused_moe's logic on the host clock: one installed plan per power-of-two bucket,
+    each a height the shape has a kernel for (256-row tiles among the packed candidates), the
+    installed plans keep parity with the oracle, and clearing restores the static table."""
+    from tinyserve_amd import kernels
+    H, E, I, k = 256, 8, 512, 2
+    x, gw, w13, w2 = make_layer(8, H, E, I, torch.bfloat16, seed=6)
+    a, b = tsm.pack_moe_weights(w13, w2) if packed else (w13, w2)
+    before = {T: kernels.moe_block_m(T, H, I, E, k, packed) for T in (1, 40, 300)}
+    try:
+        table = kernels.autotune_fused_moe(a, b, k, 300, packed=packed, reps=1)
+        assert set(table) == {1 << (n.bit_length() - 1) for n in (2, 4, 8, 16, 32, 64, 128, 256,
+                                                                     512, 600)}
+        for bucket, (bm, _) in table.items():
+            assert bm in ((0, 16, 64, 128, 256) if packed else (0, 16, 64)), (bucket, bm)
+        for T in (1, 40, 300):
+            bm, _ = table[1 << ((T * k).bit_length() - 1)]
+            assert kernels.moe_block_m(T, H, I, E, k, packed) == bm
+            xs = torch.randn(T, H, generator=torch.Generator().manual_seed(T)).bfloat16()
+            w, ids, _ = tsm.moe_router(xs, gw, k, True)
+            fn = tsm.fused_moe_packed if packed else tsm.fused_moe
+            close(fn(xs, a, b, w, ids), moe_reference(xs, w13, w2, w, ids.long()))
+    finally:
+        kernels.set_moe_block_m(1, 1 << 30, -1, packed)
+    assert {T: kernels.moe_block_m(T, H, I, E, k, packed) for T in (1, 40, 300)} == before
 
 
 def test_expert_parallel_and_rows(tsm):
@@ -152,6 +184,30 @@ def test_padded_shapes(tsm):
     assert out.shape == (9, 200)
     w, ids, _ = tsm.moe_router(x, gw, 4, True)
     close(out, moe_reference(x, w13, w2, w, ids.long()))
+
+
+def test_padded_pack_cache(tsm):
+    """Reference-layout weights the kernels do not take as they are (I = 96) are packed with
+    zero padding once per weight tensor: repeated calls reuse the copy, an in-place update of
+    the weights rebuilds it, and the copy is dropped with the weights."""
+    import gc
+    from tinyserve_amd import ops
+    x, gw, w13, w2 = make_layer(20, 256, 8, 96, torch.bfloat16, seed=4)
+    w, ids, _ = tsm.moe_router(x, gw, 2, True)
+    first = tsm.fused_moe(x, w13, w2, w, ids)
+    entry = ops._padded_cache[id(w13)]
+    again = tsm.fused_moe(x, w13, w2, w, ids)          # the repeated lookup
+    assert torch.equal(first, again) and ops._padded_cache[id(w13)] is entry
+    with torch.no_grad():
+        w2.mul_(2)                                       # version moves: repacked
+    twice = tsm.fused_moe(x, w13, w2, w, ids)
+    assert ops._padded_cache[id(w13)] is not entry
+    close(twice, moe_reference(x, w13, w2, w, ids.long()))
+    assert not torch.equal(twice, first)
+    key = id(w13)
+    del w13, entry
+    gc.collect()
+    assert key not in ops._padded_cache
 
 
 def test_fp32_layer(tsm):

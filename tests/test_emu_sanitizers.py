@@ -23,7 +23,7 @@ sys.path.insert(0, os.path.join(HERE, "emu"))
 import build_emu  # noqa: E402
 import harness  # noqa: E402
 
-QUICK = "not end_to_end and not every_plan or every_plan and 2"
+QUICK = "not end_to_end and not autotune and not every_plan or every_plan and 2"
 SANITIZERS = ["asan", "tsan"]
 
 

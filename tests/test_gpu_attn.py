@@ -91,6 +91,7 @@ def test_paged_attention_against_oracle(dev, H, Hkv, D, page, q_lens, kv_lens):
     attn_close(out, ref, "paged attention")
 
 
+@pytest.mark.emu_skip("HIP graph capture")
 def test_paged_attention_graph_replay(dev):
     """A decode step's attention captured in a HIP graph replays with new lengths and pages
     (the grid depends only on T, num_seqs and Hkv)."""

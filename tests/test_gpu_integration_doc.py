@@ -7,6 +7,7 @@ from test_integration_doc import binding_source as _binding_source
 pytestmark = pytest.mark.gpu
 
 
+@pytest.mark.emu_skip("the binding loads the GPU library and takes the current HIP stream")
 @pytest.mark.parametrize("with_map", [False, True])
 def test_documented_binding(dev, tsm, with_map):
     ns = {}

@@ -260,18 +260,26 @@ def _fused_moe_impl(x, w13, w2, topk_weights, topk_ids, sum_topk, packed):
 
 
 # Zero-padded packed copies made for reference-layout weights whose shape the kernels do not take
-# as it is, one per weight tensor (dropped with it), rebuilt when its version counter moves.
-_padded_cache: "weakref.WeakKeyDictionary" = weakref.WeakKeyDictionary()
+# as it is, one per weight tensor (dropped with it), rebuilt when either tensor's storage or
+# version counter moves. Keyed by id() with a weak reference checked by identity: a
+# WeakKeyDictionary would compare two tensors with == (elementwise) on a repeated lookup.
+_padded_cache: dict = {}
 
 
 def _padded_pack_cached(w13, w2):
-    key = (w2.data_ptr(), w13._version, w2._version)
-    hit = _padded_cache.get(w13)
-    if hit is not None and hit[0] == key:
-        return hit[1]
+    key = (w13.data_ptr(), w2.data_ptr(), w13._version, w2._version)
+    hit = _padded_cache.get(id(w13))
+    if hit is not None and hit[0]() is w13 and hit[1] == key:
+        return hit[2]
     with torch.no_grad():
         p = pack_moe_weights(w13, w2)
-    _padded_cache[w13] = (key, p)
+    i = id(w13)
+
+    def drop(r, i=i):
+        if _padded_cache.get(i, (None,))[0] is r:
+            del _padded_cache[i]
+
+    _padded_cache[i] = (weakref.ref(w13, drop), key, p)
     return p
 
 
