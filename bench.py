@@ -122,6 +122,9 @@ def main():
                     help="HBM traffic per gate_up launch measured with rocprofv3 --pmc")
     ap.add_argument("--block-m", type=int, default=None,
                     help="stage timing with this tile height (0 = expert-major) instead of the plan's")
+    ap.add_argument("--no-autotune", action="store_true",
+                    help="keep the library's static plan table (by default the expert plans are "
+                         "tuned first, as the engine does at start-up: serve.py:1692-1705)")
     ap.add_argument("--profile", action="store_true",
                     help="eager stage launches only (for rocprofv3 runs); no sweep, no CPU leg")
     args = ap.parse_args()
@@ -174,6 +177,17 @@ def main():
     log("packing weights (MFMA-tiled copies)")
     packed = [tsm.pack_moe_weights(w13, w2) for (_, w13, w2) in layers]
     torch.cuda.synchronize()
+
+    plans = None
+    if not args.no_autotune:
+        from tinyserve_amd import kernels
+        log("autotuning the expert plans (both weight layouts, batches up to 8192 tokens)")
+        plans = {}
+        for name, (a, b), is_packed in (("packed", packed[0], True),
+                                        ("reference", layers[0][1:], False)):
+            table = kernels.autotune_fused_moe(a, b, K_TOP, 8192, packed=is_packed)
+            plans[name] = {str(k): bm for k, (bm, _) in sorted(table.items())}
+        log(json.dumps(plans))
 
     def forward(i, x, bias, use_packed):
         gw = layers[i][0]
@@ -375,7 +389,10 @@ def main():
         "config": {"workload": f"Qwen3-30B-A3B MoE layer decode, T={T} tokens", "tokens": T,
                    "hidden": H, "experts": E, "top_k": K_TOP, "moe_intermediate": I,
                    "norm_topk_prob": True, "layer_copies": L, "block_m": bm,
-                   "n_touched": n_touched},
+                   "n_touched": n_touched,
+                   # tile height per power-of-two bucket of T*top_k, installed by autotuning
+                   # before any timing (null: the static table)
+                   "moe_plans": plans},
         "us_per_layer": ms * 1e3,
         "tokens_per_s": T / t,
         "tflops": F / t / 1e12,
@@ -399,7 +416,8 @@ def main():
                           "TFLOPS": Fs / ts / 1e12, "frac_hbm": Bs / ts / HBM_PEAK,
                           "frac_mfma": Fs / ts / MFMA_BF16_PEAK,
                           "frac_roofline": max(Bs / HBM_PEAK, Fs / MFMA_BF16_PEAK) / ts,
-                          "n_touched": nt})
+                          "n_touched": nt,
+                          "block_m": int(lib.tsm_moe_block_m(Ts, H, I, E, K_TOP, 1))})
             log(json.dumps(sweep[-1]))
         for kind in ("zipf", "half_empty"):
             gen = torch.Generator().manual_seed(1)
@@ -416,7 +434,8 @@ def main():
             sweep.append({"tokens": 2048, "stress": kind, "us": mss * 1e3, "GBps": Bs / ts / 1e9,
                           "TFLOPS": Fs / ts / 1e12,
                           "frac_roofline": max(Bs / HBM_PEAK, Fs / MFMA_BF16_PEAK) / ts,
-                          "n_touched": nt})
+                          "n_touched": nt,
+                          "block_m": int(lib.tsm_moe_block_m(2048, H, I, E, K_TOP, 1))})
             log(json.dumps(sweep[-1]))
         res["sweep"] = sweep
 

@@ -273,13 +273,21 @@ def test_attention_side(tsm):
 
 
 def test_end_to_end_driver(tsm):
-    """The qwen3_moe driver (prefill, then decode steps) on a two-layer model: its greedy tokens
-    equal the decoder oracle's wherever the oracle's top two logits are apart."""
+    """The qwen3_moe driver (start-up plan tuning, prefill, then decode steps) on a two-layer
+    model: its greedy tokens equal the decoder oracle's wherever the oracle's top two logits are
+    apart."""
     from test_gpu_e2e import reference_logits, small_cfg
+    from tinyserve_amd import kernels
     from tinyserve_amd.e2e import build_model, generate
     model = build_model(small_cfg(), device="cpu", seed=3, router_logits="fp32")
     prompts = torch.randint(0, 1000, (2, 20), generator=torch.Generator().manual_seed(7))
-    toks, _, _ = generate(model, prompts, 4, graph=False)
+    try:
+        plans = model.autotune(40, reps=1)     # the whole prefill: 2 x 20 tokens
+        assert 1 << ((40 * model.cfg.num_experts_per_tok).bit_length() - 1) in plans
+        toks, _, _ = generate(model, prompts, 4, graph=False)
+    finally:
+        kernels.set_moe_block_m(1, 1 << 30, -1, True)
+        kernels.set_moe_block_m(1, 1 << 30, -1, False)
     ref, gaps = reference_logits(model, torch.cat([prompts, toks[:, :-1]], 1), True)
     steps = ref[:, 19:]
     top2 = steps.topk(2, dim=-1).values

@@ -120,6 +120,17 @@ class Qwen3MoeModel(nn.Module):
         for layer in self.layers:
             layer.mlp.pack()
 
+    @torch.inference_mode()
+    def autotune(self, max_num_tokens, reps=5):
+        """Time the expert plans per batch-size bucket and install the fastest, as the reference
+        engine does at start-up before capturing graphs (serve.py:1692-1705: autotune_fused_moe
+        on the first layer's weights; every layer has the same shapes). Returns the table."""
+        from .kernels import autotune_fused_moe
+        mlp = self.layers[0].mlp
+        w13, w2 = mlp.pack() if mlp.packed else (mlp.w13, mlp.w2)
+        return autotune_fused_moe(w13, w2, mlp.top_k, max_num_tokens, packed=mlp.packed,
+                                  reps=reps)
+
     def new_caches(self, num_pages, page=16):
         c = self.cfg
         return [PagedKVCache.allocate(num_pages, page, c.num_key_value_heads, c.head_dim,
@@ -259,9 +270,12 @@ def build_model(cfg=None, device="cuda", seed=0, router_logits="model", max_posi
     return model
 
 
-def run_e2e(batch=64, prompt_len=512, new_tokens=256, cfg=None, seed=0):
-    """Config 5 of the benchmark set: returns a dict of timings and throughputs."""
+def run_e2e(batch=64, prompt_len=512, new_tokens=256, cfg=None, seed=0, autotune=True):
+    """Config 5 of the benchmark set: returns a dict of timings and throughputs. With `autotune`
+    the expert plans are tuned first for batches up to the whole prefill (batch * prompt_len
+    tokens), as the reference engine tunes for max_num_batched_tokens at start-up."""
     model = build_model(cfg, seed=seed)
+    plans = model.autotune(batch * prompt_len) if autotune else None
     g = torch.Generator(device="cuda").manual_seed(seed + 1)
     prompts = torch.randint(0, model.cfg.vocab_size, (batch, prompt_len), device="cuda",
                             generator=g)
@@ -272,4 +286,5 @@ def run_e2e(batch=64, prompt_len=512, new_tokens=256, cfg=None, seed=0):
             "prefill_s": tp, "prefill_tokens_per_s": batch * prompt_len / tp,
             "decode_s": td, "decode_tokens_per_s": batch * (new_tokens - 1) / td,
             "decode_ms_per_step": td / max(new_tokens - 1, 1) * 1e3,
-            "first_tokens": toks[0, :8].tolist()}
+            "first_tokens": toks[0, :8].tolist(),
+            "moe_plans": None if plans is None else {b: bm for b, (bm, _) in plans.items()}}
