@@ -126,7 +126,8 @@ def main():
                     help="keep the library's static plan table (by default the expert plans are "
                          "tuned first, as the engine does at start-up: serve.py:1692-1705)")
     ap.add_argument("--profile", action="store_true",
-                    help="eager stage launches only (for rocprofv3 runs); no sweep, no CPU leg")
+                    help="stage launches only (for rocprofv3 runs; the static plans, or "
+                         "--block-m, without tuning launches in the trace); no sweep, no CPU leg")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path "
@@ -179,7 +180,7 @@ def main():
     torch.cuda.synchronize()
 
     plans = None
-    if not args.no_autotune:
+    if not (args.no_autotune or args.profile):   # profile runs: the static plans or --block-m
         from tinyserve_amd import kernels
         log("autotuning the expert plans (both weight layouts, batches up to 8192 tokens)")
         plans = {}
