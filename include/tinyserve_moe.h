@@ -254,18 +254,24 @@ int tsm_qk_norm_rope(void* q, int64_t T, int H, int64_t q_tok_stride, int64_t q_
  * reference, but a wrong entry cannot address memory outside the caches).
  * Requests with one query token run in one launch (each workgroup's four wavefronts split the
  * context), longer ones in a second (skipped when max_query_len <= 1); the grids depend on T,
- * num_seqs and Hkv only, so a step can be captured in a HIP graph.
+ * num_seqs, Hkv and num_splits only, so a step can be captured in a HIP graph.
+ * Split-KV (num_splits > 1, at most 64): the one-token requests' contexts are cut into
+ * num_splits contiguous ranges of 32-key blocks, one workgroup each, whose normalised partial
+ * outputs and log-sum-exps go to `ws` (tsm_paged_attention_workspace_size bytes, 256-byte
+ * aligned; unused with one split) and are merged in split order by a second launch, as the
+ * reference's split-KV decode (_num_splits / _combine_splits_kernel, tinykernels.py:801-889).
  * Replaces paged_attention / _paged_attn_kernel (tinykernels.py:309-1028); results are those
  * of torch_ref_attention (serve.py:639-688). Requires D in {64, 128}, H / Hkv dividing 16,
  * page % 4 == 0, 16-byte aligned q rows.
  */
+size_t tsm_paged_attention_workspace_size(int num_seqs, int H, int D, int num_splits);
 int tsm_paged_attention(const void* q, int64_t T, int H, int64_t q_tok_stride,
                         int64_t q_head_stride, const void* k_cache, const void* v_cache,
                         int64_t num_pages, int page, int Hkv, int D, const int32_t* query_start_loc,
                         const int32_t* cu_seqlens_k, const int32_t* block_table,
                         int64_t bt_stride, int num_seqs, int max_query_len, float scale,
-                        void* out, int64_t o_tok_stride, int64_t o_head_stride,
-                        hipStream_t stream);
+                        int num_splits, void* ws, size_t ws_bytes, void* out,
+                        int64_t o_tok_stride, int64_t o_head_stride, hipStream_t stream);
 
 /*
  * Greedy token choice: out[r] = the index of the largest of logits[r, 0..V) (row stride ld,

@@ -53,6 +53,12 @@ def emulated(sanitizer: str = None):
 
     no_check = lambda *ts: None  # noqa: E731
     patch(ops, "torch", _AlignedTorch())
+    patch(attention, "torch", _AlignedTorch())
+    # the split-KV choice asks for the device's CU count: the emulated device has MI355X's 256
+    choose = attention.choose_num_splits
+    patch(attention, "choose_num_splits",
+          lambda programs, max_seq_len, device: choose(programs, max_seq_len, "cuda:0"))
+    patch(attention, "_cu_counts", {0: 256})
     no_stream = lambda t=None: None  # noqa: E731
     for mod in (L, ops, attention, kernels):
         patch(mod, "lib", emu)

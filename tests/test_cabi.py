@@ -132,16 +132,26 @@ def test_attention_validation(lib):
     P, I64, I32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
     f = lib.tsm_paged_attention
     f.argtypes = [P, I64, I32, I64, I64, P, P, I64, I32, I32, I32, P, P, P, I64, I32, I32,
-                  ctypes.c_float, P, I64, I64, P]
-    args = lambda H, Hkv, D=128, page=16: (P(256), 4, H, H * D, D, P(256), P(256), 8, page,  # noqa
-                                            Hkv, D, P(256), P(256), P(256), 4, 2, 1, 0.1,
-                                            P(256), H * D, D, None)
+                  ctypes.c_float, I32, P, ctypes.c_size_t, P, I64, I64, P]
+    args = lambda H, Hkv, D=128, page=16, S=1, ws=None, nws=0: (  # noqa
+        P(256), 4, H, H * D, D, P(256), P(256), 8, page, Hkv, D, P(256), P(256), P(256), 4, 2,
+        1, 0.1, S, ws, nws, P(256), H * D, D, None)
     assert f(*args(0, 4)) == -1
     assert f(*args(32, 0)) == -1
     assert f(*args(2, 4)) == -1           # fewer query heads than KV heads
     assert f(*args(32 * 3, 3)) == -2      # group 32 does not divide 16
     assert f(*args(32, 4, D=96)) == -2    # head_dim
     assert f(*args(32, 4, page=6)) == -2  # page % 4
+    # split-KV: split count range, and the workspace it needs
+    ws = lib.tsm_paged_attention_workspace_size
+    ws.argtypes, ws.restype = [I32, I32, I32, I32], ctypes.c_size_t
+    assert ws(2, 32, 128, 1) == 0 and ws(2, 32, 128, 0) == 0 and ws(2, 32, 128, 65) == 0
+    need = ws(2, 32, 128, 8)
+    assert need == 2 * 32 * 8 * 128 * 4 + 2 * 32 * 8 * 4
+    assert f(*args(32, 4, S=0)) == -1 and f(*args(32, 4, S=65)) == -1
+    assert f(*args(32, 4, S=8)) == -4                                 # no workspace
+    assert f(*args(32, 4, S=8, ws=P(256), nws=need - 1)) == -4        # too small
+    assert f(*args(32, 4, S=8, ws=P(264), nws=need)) == -4            # not 256-byte aligned
 
 
 def test_128_row_plan_only_where_the_tile_kernels_run(lib):

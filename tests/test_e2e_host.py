@@ -90,3 +90,16 @@ def test_decoder_reference_is_causal_and_attention_is_textbook():
         sd["lm_head.weight"].double().t()
     out = decoder_reference(sd, cfg, ids)[0].double()
     assert (out - ref).abs().max() <= 0.05 * ref.abs().max()
+
+
+def test_split_count_choice():
+    """The reference's rule: about two workgroups per CU, splits of >= 256 keys, at most 16,
+    a power of two; no split without a known context bound."""
+    from tinyserve_amd import attention
+    attention._cu_counts[0] = 256
+    assert attention.choose_num_splits(4, 8192, "cuda:0") == 16
+    assert attention.choose_num_splits(4, 1000, "cuda:0") == 4     # 1000 // 256 = 3 -> 4
+    assert attention.choose_num_splits(256, 8192, "cuda:0") == 2
+    assert attention.choose_num_splits(512, 8192, "cuda:0") == 1
+    assert attention.choose_num_splits(4, 300, "cuda:0") == 1
+    assert attention.choose_num_splits(4, None, "cuda:0") == 1

@@ -248,10 +248,12 @@ def test_attention_side(tsm):
                                     (8, 4, 64, 8, [3, 1, 17, 2], [9, 129, 17, 2]),
                                     (16, 1, 128, 32, [7, 1], [100, 300])]:
         q, kc, vc, cache, bt, qsl = build_batch("cpu", ql, kl, H, Hkv, D, page, seed=H + D)
-        out = paged_attention(q, cache, Meta("cpu", qsl, kl, bt), D ** -0.5).float()
         ref = paged_attention_ref(q.float(), kc.float(), vc.float(), qsl, kl, bt, D ** -0.5)
-        assert torch.isfinite(out).all()
-        assert bool(((out - ref).abs() <= 8e-3 + ref.abs() * 2.0 ** -7).all())
+        for splits in (1, 4, 16):   # split-KV decode: 16 leaves splits empty at these lengths
+            out = paged_attention(q, cache.k, cache.v, Meta("cpu", qsl, kl, bt), D ** -0.5,
+                                  num_splits=splits).float()
+            assert torch.isfinite(out).all()
+            assert bool(((out - ref).abs() <= 8e-3 + ref.abs() * 2.0 ** -7).all()), splits
     T, H, Hkv, D = 5, 8, 2, 64
     g = torch.Generator().manual_seed(1)
     qkv = (torch.randn(T, (H + 2 * Hkv) * D, generator=g) * 3).bfloat16()
@@ -264,7 +266,7 @@ def test_attention_side(tsm):
     dq, dk, dv = (t.view(T, -1, D) for t in d.split([H * D, Hkv * D, Hkv * D], -1))
     cache = PagedKVCache.allocate(4, 16, Hkv, D, "cpu")
     slots = torch.tensor([16, 17, 40, -1, 6000])          # -1 and past the pool: not written
-    qk_norm_rope(dq, dk, ang.cos(), ang.sin(), qw, kw, 1e-6, dv, cache, slots)
+    qk_norm_rope(dq, dk, ang.cos(), ang.sin(), qw, kw, 1e-6, dv, cache.k, cache.v, slots)
     assert torch.equal(dq, rq) and torch.equal(dk, rk)
     assert torch.equal(cache.k[1, 0], dk[0]) and torch.equal(cache.v[2, :, :, 8], v[2])
     x = torch.randn(6, 1000, generator=g)

@@ -86,9 +86,33 @@ def test_paged_attention_against_oracle(dev, H, Hkv, D, page, q_lens, kv_lens):
     print(f"attention H={H} Hkv={Hkv} D={D} page={page} q={q_lens} kv={kv_lens}", flush=True)
     q, kc, vc, cache, bt, qsl = build_batch(dev, q_lens, kv_lens, H, Hkv, D, page, seed=H + D)
     meta = Meta(dev, qsl, kv_lens, bt)
-    out = paged_attention(q.to(dev), cache, meta, D ** -0.5)
+    out = paged_attention(q.to(dev), cache.k, cache.v, meta, D ** -0.5)
     ref = paged_attention_ref(q.float(), kc.float(), vc.float(), qsl, kv_lens, bt, D ** -0.5)
     attn_close(out, ref, "paged attention")
+
+
+# split-KV decode: (H, Hkv, D, page, q_lens, kv_lens, num_splits); 33 keys over 16 splits leaves
+# most splits empty, the mixed batch keeps its prefill request on the unsplit launch
+SPLIT_CASES = [
+    (32, 4, 128, 16, [1], [4000], 16),
+    (32, 4, 128, 16, [1, 1, 1], [33, 1000, 1], 16),
+    (8, 4, 64, 8, [1, 1, 5, 1], [700, 1, 300, 2049], 4),
+    (16, 1, 128, 32, [1, 1], [257, 64], 2),
+]
+
+
+@pytest.mark.parametrize("H,Hkv,D,page,q_lens,kv_lens,splits", SPLIT_CASES)
+def test_split_kv_decode_against_oracle(dev, H, Hkv, D, page, q_lens, kv_lens, splits):
+    from tinyserve_amd.attention import paged_attention
+    print(f"split-KV H={H} Hkv={Hkv} D={D} q={q_lens} kv={kv_lens} splits={splits}", flush=True)
+    q, kc, vc, cache, bt, qsl = build_batch(dev, q_lens, kv_lens, H, Hkv, D, page, seed=splits)
+    meta = Meta(dev, qsl, kv_lens, bt)
+    ref = paged_attention_ref(q.float(), kc.float(), vc.float(), qsl, kv_lens, bt, D ** -0.5)
+    out = paged_attention(q.to(dev), cache.k, cache.v, meta, D ** -0.5, num_splits=splits)
+    attn_close(out, ref, f"{splits} splits")
+    # the automatic choice from max_seq_len (a small batch of long contexts splits)
+    meta.max_seq_len = max(kv_lens)
+    attn_close(paged_attention(q.to(dev), cache.k, cache.v, meta, D ** -0.5), ref, "auto")
 
 
 @pytest.mark.emu_skip("HIP graph capture")
@@ -101,15 +125,15 @@ def test_paged_attention_graph_replay(dev):
                                             seed=5, nan_tail=False)
     meta = Meta(dev, qsl, [50, 200, 17, 400], bt)
     qd = q.to(dev)
-    eager = paged_attention(qd, cache, meta, D ** -0.5)
+    eager = paged_attention(qd, cache.k, cache.v, meta, D ** -0.5)
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
-        paged_attention(qd, cache, meta, D ** -0.5)
+        paged_attention(qd, cache.k, cache.v, meta, D ** -0.5)
     torch.cuda.current_stream().wait_stream(s)
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
-        out = paged_attention(qd, cache, meta, D ** -0.5)
+        out = paged_attention(qd, cache.k, cache.v, meta, D ** -0.5)
     for _ in range(3):
         graph.replay()
         torch.cuda.synchronize()
@@ -148,7 +172,7 @@ def test_qk_norm_rope_and_cache_write(dev, T, H, Hkv, D, norm):
     dq, dk, dv = d_qkv.split([H * D, Hkv * D, Hkv * D], dim=-1)
     dq, dk, dv = dq.view(T, H, D), dk.view(T, Hkv, D), dv.view(T, Hkv, D)   # strided views
     qk_norm_rope(dq, dk, cos.to(dev), sin.to(dev), None if qw is None else qw.to(dev),
-                 None if kw is None else kw.to(dev), 1e-6, dv, cache, slots.to(dev))
+                 None if kw is None else kw.to(dev), 1e-6, dv, cache.k, cache.v, slots.to(dev))
     ulp_close(dq, rq)
     ulp_close(dk, rk)
     assert torch.equal(dv.cpu(), v)   # v itself is left alone

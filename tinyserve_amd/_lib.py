@@ -49,7 +49,8 @@ SIGNATURES = {
     "tsm_qk_norm_rope": ([P, I64, I32, I64, I64, P, I32, I64, I64, P, I64, I64, I32, P, P, I64,
                           P, P, ctypes.c_float, P, P, I64, I32, P, P], I32),
     "tsm_paged_attention": ([P, I64, I32, I64, I64, P, P, I64, I32, I32, I32, P, P, P, I64,
-                             I32, I32, ctypes.c_float, P, I64, I64, P], I32),
+                             I32, I32, ctypes.c_float, I32, P, SZ, P, I64, I64, P], I32),
+    "tsm_paged_attention_workspace_size": ([I32, I32, I32, I32], SZ),
     "tsm_greedy_argmax": ([P, I32, I64, I64, I32, P, P], I32),
     "tsm_add_rmsnorm": ([P, I64, I32, I32, P, I32, P, ctypes.c_float, P, P], I32),
     "tsm_moe_forward_workspace_size": ([I64, I32, I32, I32, I32], SZ),

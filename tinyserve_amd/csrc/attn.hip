@@ -103,7 +103,24 @@ struct AttnArgs {
     int64_t T;             // query rows: requests reaching past them are skipped
     int64_t num_pages;     // page indices are clamped into [0, num_pages)
     float scale_log2;      // softmax scale * log2(e)
+    int H;                 // query heads
+    // split-KV decode (gridDim.z splits > 1): per (request, head, split) the split's normalised
+    // output [B, H, S, D] and its log2-domain log-sum-exp [B, H, S], merged by
+    // attn_combine_kernel
+    float* part;
+    float* lse;
+    int splits;            // >= 1: the decode launch's gridDim.z
 };
+
+// The decode kernel's and the combine kernel's common test: a request taken by the decode
+// launch (one query token, consistent metadata).
+__device__ __forceinline__ bool decode_request(const AttnArgs& p, int b, int& q_start,
+                                               int& kv_len) {
+    q_start = p.qsl[b];
+    const int q_len = p.qsl[b + 1] - q_start;
+    kv_len = p.cu_k[b + 1] - p.cu_k[b];
+    return q_len == 1 && q_start >= 0 && q_start + 1 <= p.T && kv_len >= 1;
+}
 
 // Page of context position `pos` (< kv_len): the block-table entry, clamped into the pool, so
 // that inconsistent metadata reads a wrong page rather than memory outside the caches.
@@ -134,8 +151,11 @@ __device__ __forceinline__ float xor_max(float v) {
 //       d = 16 c + 4 (l / 16) + i, the row whose running max and sum it keeps.
 // Keys past the context are read from a valid page and masked: scores to -inf, V values to
 // zero (unused cache slots may hold anything, and 0 * NaN would be NaN).
-// DECODE: one workgroup per (request with one query token, KV head); the four wavefronts take
-// every fourth key block and their partial (max, sum, output) are merged through LDS.
+// DECODE: one workgroup per (request with one query token, KV head, split of the context); the
+// four wavefronts take every fourth key block of the split's range and their partial (max, sum,
+// output) are merged through LDS. With one split the merge is the output; with more (split-KV,
+// for batches whose B * Hkv workgroups would leave CUs idle) it is the split's partial result,
+// merged by attn_combine_kernel.
 // Otherwise: workgroups over query tiles of 4 * 16 / GROUP tokens of requests with two or more
 // query tokens; each wavefront stops at its last query's causal bound.
 template <int D, int GROUP, bool DECODE>
@@ -197,7 +217,11 @@ __global__ __launch_bounds__(kAttnWaves * 64) void paged_attn_kernel(AttnArgs p)
         kv_end = tok0 < q_len ? kv_len - q_len + last + 1 : 0;
     }
     const int nblk = (kv_end + 31) / 32;
-    const int first = DECODE ? wave : 0, stride = DECODE ? kAttnWaves : 1;
+    // split-KV: this workgroup's contiguous range of key blocks (empty ranges report nothing)
+    const int nsplit = DECODE ? p.splits : 1, split = DECODE ? (int)blockIdx.z : 0;
+    const int chunk = (nblk + nsplit - 1) / nsplit;
+    const int blk_lo = split * chunk, blk_hi = min(nblk, blk_lo + chunk);
+    const int first = DECODE ? blk_lo + wave : 0, stride = DECODE ? kAttnWaves : 1;
 
     float m_i = -__builtin_huge_valf(), l_i = 0.0f;
     f32x4 o[NDB];
@@ -205,7 +229,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void paged_attn_kernel(AttnArgs p)
     for (int c = 0; c < NDB; ++c) o[c] = f32x4{0.f, 0.f, 0.f, 0.f};
     const int64_t kc_tok = (int64_t)p.Hkv * D;
 
-    for (int kb = first; kb < nblk; kb += stride) {
+    for (int kb = first; kb < blk_hi; kb += stride) {
         const int key0 = kb * 32;
         // K operand rows (keys key0 + 16 t + r), clamped into the context for the address
         u32x4 kop[2][NDS];
@@ -329,15 +353,50 @@ __global__ __launch_bounds__(kAttnWaves * 64) void paged_attn_kernel(AttnArgs p)
             acc += a * s_o[w][row][d];
         }
         const int head = kvh * GROUP + row;
-        p.out[(int64_t)q_start * p.o_ts + (int64_t)head * p.o_hs + d] =
-            f32_to_bf16(acc / (L == 0.0f ? 1.0f : L));
+        if (nsplit == 1) {
+            p.out[(int64_t)q_start * p.o_ts + (int64_t)head * p.o_hs + d] =
+                f32_to_bf16(acc / (L == 0.0f ? 1.0f : L));
+        } else {
+            const int64_t at = ((int64_t)b * p.H + head) * nsplit + split;
+            p.part[at * D + d] = L == 0.0f ? 0.0f : acc / L;
+            if (d == 0) p.lse[at] = L == 0.0f ? -__builtin_huge_valf() : Mu + log2f(L);
+        }
     }
 }
 
+// Split-KV merge: one workgroup per (request, query head), a thread per d. The splits' outputs
+// are weighted by 2^(lse_s - max lse) in split order (fixed: deterministic), as the reference's
+// _combine_splits_kernel (tinykernels.py:801-858) merges them.
+template <int D>
+__global__ __launch_bounds__(D) void attn_combine_kernel(AttnArgs p) {
+    const int b = blockIdx.x, head = blockIdx.y, d = threadIdx.x;
+    int q_start, kv_len;
+    if (!decode_request(p, b, q_start, kv_len)) return;
+    const int S = p.splits;
+    const int64_t at0 = ((int64_t)b * p.H + head) * S;
+    float M = -__builtin_huge_valf();
+    for (int s = 0; s < S; ++s) M = fmaxf(M, p.lse[at0 + s]);
+    float W = 0.0f, acc = 0.0f;
+    if (M != -__builtin_huge_valf()) {
+        for (int s = 0; s < S; ++s) {
+            const float w = __builtin_amdgcn_exp2f(p.lse[at0 + s] - M);
+            W += w;
+            acc += w * p.part[(at0 + s) * D + d];
+        }
+    }
+    p.out[(int64_t)q_start * p.o_ts + (int64_t)head * p.o_hs + d] =
+        f32_to_bf16(acc / (W == 0.0f ? 1.0f : W));
+}
+
 template <int D, int GROUP>
-void launch_attn(const AttnArgs& a, int64_t T, int max_query_len, hipStream_t stream) {
-    hipLaunchKernelGGL((paged_attn_kernel<D, GROUP, true>), dim3((unsigned)a.B, (unsigned)a.Hkv),
+void launch_attn(const AttnArgs& a, int64_t T, int max_query_len, int splits,
+                 hipStream_t stream) {
+    hipLaunchKernelGGL((paged_attn_kernel<D, GROUP, true>),
+                       dim3((unsigned)a.B, (unsigned)a.Hkv, (unsigned)splits),
                        dim3(kAttnWaves * 64), 0, stream, a);
+    if (splits > 1)
+        hipLaunchKernelGGL((attn_combine_kernel<D>), dim3((unsigned)a.B, (unsigned)a.H),
+                           dim3(D), 0, stream, a);
     if (max_query_len > 1) {
         constexpr int TQ = kAttnWaves * (16 / GROUP);
         const int64_t tiles = T / TQ + a.B;
@@ -348,14 +407,14 @@ void launch_attn(const AttnArgs& a, int64_t T, int max_query_len, hipStream_t st
 }
 
 template <int D>
-bool launch_attn_d(const AttnArgs& a, int group, int64_t T, int max_query_len,
+bool launch_attn_d(const AttnArgs& a, int group, int64_t T, int max_query_len, int splits,
                    hipStream_t stream) {
     switch (group) {
-        case 1: launch_attn<D, 1>(a, T, max_query_len, stream); return true;
-        case 2: launch_attn<D, 2>(a, T, max_query_len, stream); return true;
-        case 4: launch_attn<D, 4>(a, T, max_query_len, stream); return true;
-        case 8: launch_attn<D, 8>(a, T, max_query_len, stream); return true;
-        case 16: launch_attn<D, 16>(a, T, max_query_len, stream); return true;
+        case 1: launch_attn<D, 1>(a, T, max_query_len, splits, stream); return true;
+        case 2: launch_attn<D, 2>(a, T, max_query_len, splits, stream); return true;
+        case 4: launch_attn<D, 4>(a, T, max_query_len, splits, stream); return true;
+        case 8: launch_attn<D, 8>(a, T, max_query_len, splits, stream); return true;
+        case 16: launch_attn<D, 16>(a, T, max_query_len, splits, stream); return true;
         default: return false;
     }
 }
@@ -450,16 +509,34 @@ extern "C" int tsm_qk_norm_rope(void* q, int64_t T, int H, int64_t q_tok_stride,
     return check_launch("qk_norm_rope_kernel");
 }
 
+namespace {
+constexpr int kMaxSplits = 64;
+
+// split-KV workspace: partial outputs [B, H, S, D] fp32, then the log-sum-exps [B, H, S] fp32
+size_t attn_part_bytes(int64_t B, int H, int D, int S) {
+    return ((size_t)B * H * S * D * sizeof(float) + 255) / 256 * 256;
+}
+}  // namespace
+
+extern "C" size_t tsm_paged_attention_workspace_size(int num_seqs, int H, int D, int num_splits) {
+    if (num_seqs < 0 || H < 1 || D < 1 || num_splits < 1 || num_splits > kMaxSplits) return 0;
+    if (num_splits == 1) return 0;
+    return attn_part_bytes(num_seqs, H, D, num_splits) +
+           (size_t)num_seqs * H * num_splits * sizeof(float);
+}
+
 extern "C" int tsm_paged_attention(const void* q, int64_t T, int H, int64_t q_tok_stride,
                                    int64_t q_head_stride, const void* k_cache,
                                    const void* v_cache, int64_t num_pages, int page, int Hkv,
                                    int D,
                                    const int32_t* query_start_loc, const int32_t* cu_seqlens_k,
                                    const int32_t* block_table, int64_t bt_stride, int num_seqs,
-                                   int max_query_len, float scale, void* out,
-                                   int64_t o_tok_stride, int64_t o_head_stride,
-                                   hipStream_t stream) {
+                                   int max_query_len, float scale, int num_splits, void* ws,
+                                   size_t ws_bytes, void* out, int64_t o_tok_stride,
+                                   int64_t o_head_stride, hipStream_t stream) {
     clear_error();
+    TSM_REQUIRE(num_splits >= 1 && num_splits <= kMaxSplits, TSM_E_ARG,
+                "num_splits must be in [1, %d] (got %d)", kMaxSplits, num_splits);
     TSM_REQUIRE(T >= 0 && T <= 0x7fffffffll && num_seqs >= 0 && num_seqs <= 65535, TSM_E_ARG,
                 "bad sizes (T=%lld B=%d)", (long long)T, num_seqs);
     TSM_REQUIRE(Hkv >= 1 && H >= Hkv && H % Hkv == 0, TSM_E_ARG,
@@ -479,6 +556,11 @@ extern "C" int tsm_paged_attention(const void* q, int64_t T, int H, int64_t q_to
                 TSM_E_ARG, "null pointer argument");
     TSM_REQUIRE(tsm_aligned(16, {q, k_cache}) && tsm_aligned(8, {v_cache, out}), TSM_E_ARG,
                 "attention needs 16-byte aligned q and K pages, 8-byte aligned V pages and out");
+    const size_t need = tsm_paged_attention_workspace_size(num_seqs, H, D, num_splits);
+    TSM_REQUIRE(num_splits == 1 || (ws && ws_bytes >= need && tsm_aligned(256, {ws})),
+                TSM_E_WORKSPACE,
+                "split-KV needs a 256-byte aligned workspace of >= %zu bytes (got %zu)", need,
+                ws_bytes);
     AttnArgs a{};
     a.q = (const bf16_t*)q;
     a.k_cache = (const bf16_t*)k_cache;
@@ -498,8 +580,15 @@ extern "C" int tsm_paged_attention(const void* q, int64_t T, int H, int64_t q_to
     a.num_pages = num_pages;
     a.T = T;
     a.scale_log2 = scale * 1.4426950408889634f;
-    const bool ok = D == 128 ? launch_attn_d<128>(a, group, T, max_query_len, stream)
-                             : launch_attn_d<64>(a, group, T, max_query_len, stream);
+    a.H = H;
+    a.splits = num_splits;
+    if (num_splits > 1) {
+        a.part = reinterpret_cast<float*>(ws);
+        a.lse = reinterpret_cast<float*>((char*)ws + attn_part_bytes(num_seqs, H, D, num_splits));
+    }
+    const bool ok =
+        D == 128 ? launch_attn_d<128>(a, group, T, max_query_len, num_splits, stream)
+                 : launch_attn_d<64>(a, group, T, max_query_len, num_splits, stream);
     TSM_REQUIRE(ok, TSM_E_SHAPE, "no attention kernel for group %d", group);
     return check_launch("paged_attn_kernel");
 }

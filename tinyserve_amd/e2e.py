@@ -62,9 +62,9 @@ class Attention(nn.Module):
         T = x.shape[0]
         q, k, v = self.qkv_proj(x).split(self.qkv_sizes, dim=-1)
         q, k, v = q.view(T, self.H, self.D), k.view(T, self.Hkv, self.D), v.view(T, self.Hkv, self.D)
-        qk_norm_rope(q, k, cos, sin, self.q_norm, self.k_norm, self.eps, v, cache,
+        qk_norm_rope(q, k, cos, sin, self.q_norm, self.k_norm, self.eps, v, cache.k, cache.v,
                      meta.slot_mapping)
-        o = paged_attention(q, cache, meta, self.D ** -0.5)
+        o = paged_attention(q, cache.k, cache.v, meta, self.D ** -0.5)
         return self.o_proj(o.view(T, self.H * self.D))
 
 
@@ -181,7 +181,7 @@ class PagedBatch:
         meta = SimpleNamespace(query_start_loc=starts, cu_seqlens_k=starts.clone(),
                                block_table=self.block_table[:len(lens)],
                                num_seqs=len(lens), max_query_len=max(lens),
-                               slot_mapping=self.slots(seq, pos))
+                               max_seq_len=max(lens), slot_mapping=self.slots(seq, pos))
         return meta, pos, starts[1:].long() - 1
 
 
@@ -219,6 +219,9 @@ def generate(model, prompts, new_tokens, graph=True, page=16, prefill_chunk=None
     meta = SimpleNamespace(query_start_loc=torch.arange(B + 1, dtype=torch.int32, device=dev),
                            cu_seqlens_k=torch.zeros(B + 1, dtype=torch.int32, device=dev),
                            block_table=batch.block_table, num_seqs=B, max_query_len=1,
+                           # the bound a captured step is valid for, as serve.py bakes
+                           # max_model_len into its graph metadata (split-KV choice)
+                           max_seq_len=P + new_tokens,
                            slot_mapping=torch.zeros(B, dtype=torch.long, device=dev))
     rows = torch.arange(B, device=dev)
 
