@@ -6,9 +6,9 @@ matrix-core instruction evaluated on the CPU). Textual adaptations are made on c
 sources, never on the sources themselves: the dynamic LDS declaration becomes a pointer to the
 emulated LDS; each static __shared__ declaration becomes a reference into the emulated
 workgroup's LDS arena (which, like the dynamic LDS, starts every workgroup as garbage); and the
-two inline-assembly idioms the tile kernel uses (a register copy that places a wait, and an
-LDS-wait + workgroup barrier, which does not wait for global->LDS loads) become their host
-equivalents. Any other inline assembly or __shared__ form stops the build.
+inline-assembly idioms the tile kernel uses (a register copy that places a wait, an LDS-wait +
+workgroup barrier, which does not wait for global->LDS loads, and an empty statement that hides
+a value from the optimiser) become their host equivalents. Any other inline assembly or __shared__ form stops the build.
 
 The result, tests/emu/_build/libtsm_emu[_asan|_tsan].so, exports the same C ABI as
 libtinyserve_moe.so and is loaded only by tests. With sanitizer="asan" every memory access of the
@@ -34,6 +34,8 @@ ASM_REWRITES = [
      r"\1 = \2;"),
     (re.compile(r'asm volatile\("s_waitcnt lgkmcnt\(0\)\\n\\ts_barrier" ::: "memory"\);'),
      "::emu::s_barrier();"),
+    # an empty asm that only hides a value from the optimiser: nothing to do on the host
+    (re.compile(r'asm volatile\(""\s*:\s*"\+[sv]"\((\w+)\)\);'), r"(void)\1;"),
 ]
 FLAGS = ["-std=c++17", "-O2", "-g", "-fPIC", "-fno-omit-frame-pointer", "-w", "-mavx2", "-mfma"]
 LDS_DECL = re.compile(r"extern __shared__[^;]*\bchar (\w+)\[\];")

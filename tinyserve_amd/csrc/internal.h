@@ -50,6 +50,8 @@ inline int64_t active_tile_bound(int64_t numel, int E, int block_m) {
 // tile_kernels_take: whether they take an (H, I) layer (the 128-row plan exists only then).
 bool tile_kernels_take(int H, int I);
 bool launch_tile_gate_up(GemmArgs g, int block_m, hipStream_t stream);
+// whether the 256-row gate_up kernel takes an x of T rows of K elements (32-bit byte offsets)
+bool tile256_takes_x(int64_t T, int K);
 bool launch_tile_down(GemmArgs g, int block_m, hipStream_t stream);
 
 // Expert-major decode kernels (no permutation step): assignments per expert are found by scanning

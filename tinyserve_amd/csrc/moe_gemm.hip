@@ -286,7 +286,8 @@ Plan plan_for(int64_t T, int H, int I, int E, int top_k, bool packed) {
         const int o = g_block_m_override[packed][numel_bucket(numel)].load(std::memory_order_relaxed);
         // an installed height applies where its kernels take the shape
         if (o == 0 && expert_path_supported(numel, H, I, E)) return Plan{0};
-        if (o > 0 && block_m_supported(o, packed) && (o < 128 || tile_kernels_take(H, I)))
+        if (o > 0 && block_m_supported(o, packed) && (o < 128 || tile_kernels_take(H, I)) &&
+            (o != 256 || tile256_takes_x(T, H)))
             return Plan{o};
     }
     if (numel >= 1 && numel <= 12ll * E && expert_path_supported(numel, H, I, E))

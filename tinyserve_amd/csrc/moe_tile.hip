@@ -101,6 +101,24 @@ __device__ __forceinline__ void interleave_reads_mfma() {
     __builtin_amdgcn_sched_group_barrier(0x008, NM - NR, 0);
 }
 
+// Schedule of a 256-row tile's second half-k-step: the FH reads of the next A half interleaved
+// with the first FH MFMAs (B block 0), then after each B block's FH MFMAs the read that refills
+// that block's B fragment for the next k-step (its last use has then issued).
+template <int FH, int FN>
+__device__ __forceinline__ void refill_sched() {
+#pragma unroll
+    for (int i = 0; i < FH; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+#pragma unroll
+    for (int g = 1; g < FN; ++g) {
+        __builtin_amdgcn_sched_group_barrier(0x008, FH, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+}
+
 // Ring: A (gathered rows) in 2 slots, B (weights, the operand streamed from HBM) in NB slots, so
 // B runs NB - 1 stages ahead and A one stage ahead. Issue order per tile: B(0..NB-3), A(0),
 // B(NB-2), then at the barrier before stage s (s >= 1) A(s+1), B(s+NB-1). When the wavefront
@@ -155,7 +173,10 @@ __global__ __launch_bounds__(64 * kNW, 1) void moe_tile_kernel(GemmArgs p) {
     // rows are the tile's own consecutive rows, so a 32-bit offset from the tile's first row,
     // a_base, which is uniform). B: instruction index w + 8j is block (nb, kk) = ((w >> 1) + 4j,
     // w & 1), so one base pointer plus j * b_jstride covers the wavefront's loads.
-    using a_off_t = typename std::conditional<GATEUP, uint64_t, uint32_t>::type;
+    // 256-row gate_up tiles use 32-bit offsets too (x below 4 GiB, checked on the host): the
+    // loads then take the uniform base in SGPRs and one offset VGPR (the register budget of
+    // these tiles has no room for 64-bit addresses).
+    using a_off_t = typename std::conditional<GATEUP && BM != 256, uint64_t, uint32_t>::type;
     a_off_t a_src[LPA];
     const bf16_t* a_base = p.A;
     const bf16_t* b_src = nullptr;
@@ -169,7 +190,11 @@ __global__ __launch_bounds__(64 * kNW, 1) void moe_tile_kernel(GemmArgs p) {
     // its stages, and settled after its last stage, when nothing else is in flight. finish()
     // turns them into load sources.
     int f_m0 = 0, f_n = 0, f_expert = -1, f_rowflat = 0;
-    int f_flat[LPA];
+    // gate_up: the sorted ids of the rows this lane gathers (load j: row (wave + 8 j) * 8 +
+    // lane / 8). 256-row tiles, whose registers are the scarcest, hold one id per lane instead
+    // (lane l: load l / 8 % 4, row l % 8) and move them to their loaders with a shuffle.
+    constexpr int NFL = BM == 256 ? 1 : LPA;
+    int f_flat[NFL];
     auto fetch = [&](int logical) {
         // column tiles fastest: the tiles that share an A block run side by side, and so do
         // the row tiles of one expert that share a B panel
@@ -180,7 +205,13 @@ __global__ __launch_bounds__(64 * kNW, 1) void moe_tile_kernel(GemmArgs p) {
         if (GATEUP) {
 #pragma unroll
             for (int j = 0; j < LPA; ++j)
-                f_flat[j] = p.sorted_ids[f_m0 + (wave + j * kNW) * 8 + (lane >> 3)];
+                if (BM == 256) {
+                    if (j == 0)
+                        f_flat[0] = p.sorted_ids[f_m0 + (wave + ((lane >> 3) & 3) * kNW) * 8 +
+                                                 (lane & 7)];
+                } else {
+                    f_flat[j] = p.sorted_ids[f_m0 + (wave + j * kNW) * 8 + (lane >> 3)];
+                }
         } else {
             f_rowflat = tid < BM ? p.sorted_ids[f_m0 + tid] : (int)p.numel;
         }
@@ -189,7 +220,7 @@ __global__ __launch_bounds__(64 * kNW, 1) void moe_tile_kernel(GemmArgs p) {
         f_expert = settle(f_expert);
         if (GATEUP) {
 #pragma unroll
-            for (int j = 0; j < LPA; ++j) f_flat[j] = settle(f_flat[j]);
+            for (int j = 0; j < NFL; ++j) f_flat[j] = settle(f_flat[j]);
         } else {
             f_rowflat = settle(f_rowflat);
         }
@@ -206,7 +237,7 @@ __global__ __launch_bounds__(64 * kNW, 1) void moe_tile_kernel(GemmArgs p) {
         for (int j = 0; j < LPA; ++j) {
             int src_row;
             if (GATEUP) {
-                int flat = f_flat[j];
+                int flat = BM == 256 ? __shfl(f_flat[0], j * 8 + (lane >> 3)) : f_flat[j];
                 if (flat >= p.numel) flat = 0;  // padding row: any valid row, discarded
                 src_row = flat / p.top_k;
             } else {
@@ -221,9 +252,16 @@ __global__ __launch_bounds__(64 * kNW, 1) void moe_tile_kernel(GemmArgs p) {
     };
     auto issue_a = [&](int st) {
         char* base = lds + (st & 1) * A_BYTES;
+        // 256: the base is made opaque to the loop so the compiler cannot hoist 64-bit
+        // addresses (two registers each) out of it; base + 32-bit byte offset selects the
+        // load form with the base in SGPRs
+        const bf16_t* ab = a_base;
+        if constexpr (BM == 256) asm volatile("" : "+s"(ab));
 #pragma unroll
         for (int j = 0; j < LPA; ++j)
-            __builtin_amdgcn_global_load_lds((const void*)(a_base + a_src[j] + st * 64),
+            __builtin_amdgcn_global_load_lds(
+                BM == 256 ? (const void*)((const char*)ab + (uint32_t)(a_src[j] * 2u + st * 128u))
+                          : (const void*)(a_base + a_src[j] + st * 64),
                                              (lds_void*)(base + (wave + j * kNW) * kBlk), 16, 0,
                                              0);
     };
@@ -316,16 +354,21 @@ __global__ __launch_bounds__(64 * kNW, 1) void moe_tile_kernel(GemmArgs p) {
     };
 
     // the halves of the A fragments (f = h * FM/2 + i) and the B fragments of one k-step
+    // per-lane read bases with the wavefront's block offsets folded in, so that the fragment
+    // offsets below are compile-time constants (immediate offsets of the LDS reads)
+    const uint32_t a_rd0 = lds0 + a_off[0] + wm * FM * 2 * kBlk;
+    const uint32_t a_rd1 = lds0 + a_off[1] + wm * FM * 2 * kBlk;
+    const uint32_t b_rd = lds0 + 2 * A_BYTES + lane * 16 + wn * FN * 2 * kBlk;
     auto read_a_half = [&](int st, int kk, int h, u32x4 (&af)[FM / 2]) {
-        const uint32_t ab = lds0 + (st & 1) * A_BYTES + a_off[kk];
+        const uint32_t ab = (kk ? a_rd1 : a_rd0) + (st & 1) * A_BYTES;
 #pragma unroll
         for (int i = 0; i < FM / 2; ++i)
-            af[i] = lds_read16(ab + (wm * FM + h * (FM / 2) + i) * 2 * kBlk);
+            af[i] = lds_read16(ab + (h * (FM / 2) + i) * 2 * kBlk);
     };
     auto read_b = [&](int st, int kk, u32x4 (&bfr)[FN]) {
-        const uint32_t bb = lds0 + 2 * A_BYTES + (st % NB) * B_BYTES + kk * kBlk + lane * 16;
+        const uint32_t bb = b_rd + (st % NB) * B_BYTES + kk * kBlk;
 #pragma unroll
-        for (int g = 0; g < FN; ++g) bfr[g] = lds_read16(bb + (wn * FN + g) * 2 * kBlk);
+        for (int g = 0; g < FN; ++g) bfr[g] = lds_read16(bb + g * 2 * kBlk);
     };
 
     f32x4 acc[FM][FN];
@@ -414,30 +457,42 @@ __global__ __launch_bounds__(64 * kNW, 1) void moe_tile_kernel(GemmArgs p) {
         } else if constexpr (FM >= 8) {
             // 256-row tiles (a 128 x 64 block per wavefront): the accumulators take half of the
             // register budget, so A is streamed in halves of FM/2 fragments instead of being
-            // double-buffered whole: the first half's MFMAs run while the second half is read,
-            // the second half's while the next k-step's first half and B are read. The two B
-            // sets alternate roles between k-steps, so a stage ends with the next one's first
-            // B set in bc.
+            // double-buffered whole (the first half's MFMAs run while the second half is read,
+            // the second half's while the next k-step's first half is read), and B is held as
+            // one set that the second half refills fragment by fragment. With two B sets the
+            // loop did not fit the 256 registers of a wavefront: the compiler spilled, and each
+            // spill reload in the stage loop waited for every outstanding load (vmcnt(0)),
+            // draining the ring twice per stage.
             constexpr int FH = FM / 2;
-            u32x4 aL[FH], aH[FH], bc[FN], bn[FN];
+            u32x4 aL[FH], aH[FH], b[FN];
+            // second half of a k-step: B-block-major MFMAs, each B fragment replaced by the
+            // next k-step's as soon as its last MFMA has issued
+            auto mfma_half_refill = [&](const u32x4 (&af)[FH], int st_n, int kk_n) {
+#pragma unroll
+                for (int g = 0; g < FN; ++g) {
+#pragma unroll
+                    for (int i = 0; i < FH; ++i)
+                        acc[FH + i][g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                            as_bf16x8(af[i]), as_bf16x8(b[g]), acc[FH + i][g], 0, 0, 0);
+                    b[g] = lds_read16(b_rd + (st_n % NB) * B_BYTES + kk_n * kBlk + g * 2 * kBlk);
+                }
+            };
             read_a_half(0, 0, 0, aL);
-            read_b(0, 0, bc);
+            read_b(0, 0, b);
             for (int st = 0; st < NST; ++st) {
                 read_a_half(st, 0, 1, aH);
-                mfma_half(0, aL, bc);
+                mfma_half(0, aL, b);
                 interleave_reads_mfma<FH, FH * FN>();
                 read_a_half(st, 1, 0, aL);
-                read_b(st, 1, bn);
-                mfma_half(1, aH, bc);
-                interleave_reads_mfma<FH + FN, FH * FN>();
+                mfma_half_refill(aH, st, 1);
+                refill_sched<FH, FN>();
                 read_a_half(st, 1, 1, aH);
-                mfma_half(0, aL, bn);
+                mfma_half(0, aL, b);
                 interleave_reads_mfma<FH, FH * FN>();
                 if (st + 1 < NST) advance(st);
                 read_a_half(st + 1, 0, 0, aL);
-                read_b(st + 1, 0, bc);
-                mfma_half(1, aH, bn);
-                interleave_reads_mfma<FH + FN, FH * FN>();
+                mfma_half_refill(aH, st + 1, 0);
+                refill_sched<FH, FN>();
             }
         } else {
             u32x4 a0[FM], b0[FN], a1[FM], b1[FN];
@@ -601,8 +656,12 @@ bool tile_kernels_take(int H, int I) {
     return H % 64 == 0 && (2 * I) % kBN == 0 && I % 64 == 0 && H % kBN == 0;
 }
 
+bool tile256_takes_x(int64_t T, int K) { return T * (int64_t)K * 2 < (1ll << 32); }
+
 bool launch_tile_gate_up(GemmArgs g, int block_m, hipStream_t stream) {
     if (g.K % 64 != 0 || (2 * g.N) % kBN != 0) return false;
+    // the 256-row kernel gathers x rows through 32-bit byte offsets
+    if (block_m == 256 && !tile256_takes_x((g.numel + g.top_k - 1) / g.top_k, g.K)) return false;
     g.n_tiles = 2 * g.N / kBN;
     if (block_m == 256) launch_tile<256, true>(g, stream);
     else if (block_m == 128) launch_tile<128, true>(g, stream);
