@@ -55,3 +55,16 @@ def test_traffic(tmp_path):
     res = json.loads(buf.getvalue())
     assert res["fetch_factor"] == 0.5 and res["write_factor"] == 1.0
     assert res["traffic_bytes"] == 1100 * 1024 / 0.5 + 10 * 1024
+
+
+def test_counters_table(tmp_path):
+    _counters(tmp_path / "a.csv", "MfmaUtil", K, [30.0, 34.0])
+    _write(tmp_path / "b.csv", ["Kernel_Name", "Counter_Name", "Counter_Value"],
+           [[K, "SQ_INSTS_VALU_MFMA_MOPS_BF16", 8.0], [COPY, "MfmaUtil", 1.0]])
+    buf = io.StringIO()
+    with redirect_stdout(buf):
+        profiling.main(["counters", str(tmp_path / "a.csv"), str(tmp_path / "b.csv")])
+    lines = buf.getvalue().splitlines()
+    assert lines[0] == "| kernel | MfmaUtil | SQ_INSTS_VALU_MFMA_MOPS_BF16 |"
+    assert lines[2] == "| `moe_expert_kernel<16, 2, 1, true, true, 1>` | 32 | 8 |"
+    assert len(lines) == 3  # the copy kernel is not this package's

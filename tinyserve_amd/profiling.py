@@ -6,6 +6,9 @@
             --copy-fetch CF.csv --copy-write CW.csv --copy-bytes N --kernel SUBSTR
         HBM bytes per dispatch of one kernel from FETCH_SIZE / WRITE_SIZE counter collections,
         each scaled by the factor the same counter shows for a plain device copy of N bytes
+    python -m tinyserve_amd.profiling counters <run_counter_collection.csv> ... [--match SUBSTR ...]
+        markdown table of every counter's mean per dispatch, per kernel (e.g. MfmaUtil and
+        SQ_INSTS_VALU_MFMA_MOPS_BF16 of the tile kernels), over one or more collections
 """
 import argparse
 import collections
@@ -54,7 +57,27 @@ def main(argv=None):
         t.add_argument(a, required=True)
     t.add_argument("--copy-bytes", type=int, required=True)
     t.add_argument("--copy-kernel", default="copy")
+    c = sub.add_parser("counters")
+    c.add_argument("csv", nargs="+")
+    c.add_argument("--match", nargs="*", default=["tsm::"])
     args = ap.parse_args(argv)
+
+    if args.cmd == "counters":
+        table = collections.defaultdict(dict)
+        for path in args.csv:
+            agg = collections.defaultdict(list)
+            for r in csv.DictReader(open(path)):
+                if any(m in r["Kernel_Name"] for m in args.match):
+                    agg[(r["Kernel_Name"], r["Counter_Name"])].append(float(r["Counter_Value"]))
+            for (k, name), v in agg.items():
+                table[k][name] = sum(v) / len(v)
+        names = sorted({n for row in table.values() for n in row})
+        print("| kernel | " + " | ".join(names) + " |")
+        print("|---|" + "---:|" * len(names))
+        for k in sorted(table):
+            cells = [f"{table[k][n]:.4g}" if n in table[k] else "" for n in names]
+            print(f"| `{short_name(k)}` | " + " | ".join(cells) + " |")
+        return 0
 
     if args.cmd == "stats":
         print("| kernel | calls | avg us | total us |")
