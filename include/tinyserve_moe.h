@@ -142,7 +142,7 @@ int tsm_fused_moe(const void* x, const void* w13, const void* w2, const float* t
  * The stages of tsm_fused_moe, for callers that schedule them separately (and for per-kernel
  * timing). Each is one launch of the corresponding stage of _moe_gemm / _fused_moe_kernel
  * (tinykernels.py:1746-1765, 1589-1744) on the outputs of tsm_moe_align for the same block_m
- * (supported: 16, 64; 128 and 256 with packed weights):
+ * (supported: 16, 64; 128 and 256 with packed weights; gate_up at 256 needs x below 4 GiB):
  *   gate_up: act[max_padded, I] (expert-sorted rows) = bf16(bf16(silu(bf16(x W1^T))) *
  *            bf16(x W3^T)) with x gathered as x[sorted_ids[r] / top_k]; rows of remote tiles
  *            are not written.
