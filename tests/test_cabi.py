@@ -170,3 +170,21 @@ def test_128_row_plan_only_where_the_tile_kernels_run(lib):
     assert f(P(256), P(256), P(256), P(256), P(256), 512, 8, 128, 64, 32, 128, 1, P(256),
              None) == -2
     assert b"128-row" in lib.tsm_last_error()
+
+
+def test_256_row_plan_only_below_4_gib_of_x(lib):
+    """An installed 256-row plan applies only while x (T x H bf16) is below 4 GiB: the 256-row
+    gate_up kernel gathers x rows through 32-bit byte offsets. Past that, the static plan."""
+    I32, I64 = ctypes.c_int, ctypes.c_int64
+    lib.tsm_moe_set_block_m.argtypes = [I64, I64, I32, I32]
+    lib.tsm_moe_block_m.argtypes = [I64, I32, I32, I32, I32, I32]
+    H, I, E, k = 2048, 768, 128, 8
+    assert lib.tsm_moe_set_block_m(1, 1 << 30, 1, 256) == 0
+    try:
+        small = 8192
+        big = (1 << 32) // (2 * H)         # the first T with 4 GiB of x
+        assert lib.tsm_moe_block_m(small, H, I, E, k, 1) == 256
+        assert lib.tsm_moe_block_m(big - 1, H, I, E, k, 1) == 256
+        assert lib.tsm_moe_block_m(big, H, I, E, k, 1) == 128   # the static table's choice
+    finally:
+        assert lib.tsm_moe_set_block_m(1, 1 << 30, 1, -1) == 0
