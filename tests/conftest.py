@@ -24,8 +24,17 @@ def pytest_addoption(parser):
                           "layer of 512 tokens takes about 80 s on the emulation)")
 
 
+# A GPU test that has not finished in this long is hung (the largest take seconds): the thread
+# method of pytest-timeout dumps every stack, naming the test, and ends the process instead of
+# leaving it to the job's own time limit.
+GPU_TEST_TIMEOUT_S = 300
+
+
 def pytest_collection_modifyitems(config, items):
     if not config.getoption("--emulate"):
+        for item in items:
+            if item.get_closest_marker("gpu") and not item.get_closest_marker("timeout"):
+                item.add_marker(pytest.mark.timeout(GPU_TEST_TIMEOUT_S, method="thread"))
         return
     limit = config.getoption("--emulate-max-tokens")
     for item in items:
