@@ -5,7 +5,12 @@ register spill inside the stage loop breaks that: the compiler follows every spi
 a wait for *all* outstanding vector-memory operations (s_waitcnt vmcnt(0)), which drains the
 ring each stage. Results stay correct and only the speed suffers, so this is checked on the
 gfx950 assembly of the build's own source. A stage loop is a loop nested in the per-tile loop
-(depth >= 2 in the compiler's loop annotations)."""
+(depth >= 2 in the compiler's loop annotations).
+
+The 256-row kernels' stage loop is also checked for LDS latency: every fragment read there is
+consumed only several MFMAs after it issues (each 16x16x32 MFMA occupies a SIMD for about 16
+cycles at the dense rate, so 6 MFMAs cover the LDS read latency), including reads consumed in
+the next iteration."""
 import os
 import re
 import subprocess
@@ -70,3 +75,60 @@ def test_no_spills_in_stage_loops(stats):
 def test_64_and_128_row_kernels_do_not_spill_at_all(stats):
     bad = {k: v for k, v in stats.items() if "kernelILi256E" not in k and v[0]}
     assert not bad, bad
+
+
+def _regs(spec):
+    m = re.match(r"v\[(\d+):(\d+)\]", spec)
+    if m:
+        return set(range(int(m.group(1)), int(m.group(2)) + 1))
+    m = re.match(r"v(\d+)$", spec)
+    return {int(m.group(1))} if m else set()
+
+
+def _stage_loop(asm: str, kernel_re: str):
+    """Instructions of the MFMA stage loop (the depth-2 loop with the most MFMAs)."""
+    lines = asm.splitlines()
+    start = next(i for i, l in enumerate(lines) if re.match(r"^_Z\S*" + kernel_re + r"\S*:", l))
+    end = next(i for i in range(start + 1, len(lines))
+               if re.match(r"^_Z\S+:", lines[i]) or "amdhsa.kernels" in lines[i])
+    body = lines[start:end]
+    loops = []
+    for i, l in enumerate(body):
+        if "Loop Header: Depth=2" in l:
+            j = next((k for k in range(i + 1, len(body))
+                      if re.search(r"Loop: Header=BB\d+_\d+ Depth=1", body[k])), len(body))
+            loops.append(body[i:j])
+    return max(loops, key=lambda lp: sum("v_mfma" in l for l in lp))
+
+
+def _read_to_use(loop):
+    """MFMAs issued between each LDS read and the first MFMA that consumes its registers, over
+    two passes of the loop (so reads consumed by the next iteration count too)."""
+    pending, n, dists = [], 0, []
+    for line in loop + loop:
+        t = line.strip().split()
+        if not t:
+            continue
+        if t[0].startswith("ds_read"):
+            pending.append((_regs(t[1].rstrip(",")), n))
+        elif t[0].startswith("v_mfma"):
+            ops = [x.rstrip(",") for x in t[1:5]]
+            used = _regs(ops[1]) | _regs(ops[2])
+            for p in [p for p in pending if p[0] & used]:
+                dists.append(n - p[1])
+                pending.remove(p)
+            n += 1
+    return dists
+
+
+@pytest.fixture(scope="module")
+def asm(stats):
+    return _assembly()
+
+
+@pytest.mark.parametrize("gateup", [1, 0])
+def test_256_row_stage_loop_hides_lds_latency(asm, gateup):
+    loop = _stage_loop(asm, f"moe_tile_kernelILi256ELb{gateup}")
+    assert sum("v_mfma" in l for l in loop) == 64   # 2 k-steps x 8 x 4 fragments per wavefront
+    d = _read_to_use(loop)
+    assert len(d) >= 24 and min(d) >= 6, sorted(d)

@@ -372,11 +372,13 @@ __global__ __launch_bounds__(64 * kNW, 1) void moe_tile_kernel(GemmArgs p) {
     };
 
     f32x4 acc[FM][FN];
+    // B-block-major: the fragment refilled last by the previous half-k-step (block FN-1) is
+    // consumed last, at least 3 * FM/2 MFMAs after its read was issued
     auto mfma_half = [&](int h, const u32x4 (&af)[FM / 2], const u32x4 (&bfr)[FN]) {
 #pragma unroll
-        for (int i = 0; i < FM / 2; ++i)
+        for (int g = 0; g < FN; ++g)
 #pragma unroll
-            for (int g = 0; g < FN; ++g)
+            for (int i = 0; i < FM / 2; ++i)
                 acc[h * (FM / 2) + i][g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
                     as_bf16x8(af[i]), as_bf16x8(bfr[g]), acc[h * (FM / 2) + i][g], 0, 0, 0);
     };
