@@ -7,7 +7,7 @@ ring each stage. Results stay correct and only the speed suffers, so this is che
 gfx950 assembly of the build's own source. A stage loop is a loop nested in the per-tile loop
 (depth >= 2 in the compiler's loop annotations).
 
-The 256-row kernels' stage loop is also checked for LDS latency: every fragment read there is
+The prefill (128- and 256-row) kernels' stage loops are also checked for LDS latency: every fragment read there is
 consumed only several MFMAs after it issues (each 16x16x32 MFMA occupies a SIMD for about 16
 cycles at the dense rate, so 6 MFMAs cover the LDS read latency), including reads consumed in
 the next iteration."""
@@ -86,19 +86,36 @@ def _regs(spec):
 
 
 def _stage_loop(asm: str, kernel_re: str):
-    """Instructions of the MFMA stage loop (the depth-2 loop with the most MFMAs)."""
+    """Instructions of the MFMA stage loop: the blocks of the depth-2 loop with the most MFMAs,
+    in layout order rotated to start at the loop header (the compiler may place the latch block
+    before the header)."""
     lines = asm.splitlines()
     start = next(i for i, l in enumerate(lines) if re.match(r"^_Z\S*" + kernel_re + r"\S*:", l))
     end = next(i for i in range(start + 1, len(lines))
                if re.match(r"^_Z\S+:", lines[i]) or "amdhsa.kernels" in lines[i])
-    body = lines[start:end]
-    loops = []
-    for i, l in enumerate(body):
-        if "Loop Header: Depth=2" in l:
-            j = next((k for k in range(i + 1, len(body))
-                      if re.search(r"Loop: Header=BB\d+_\d+ Depth=1", body[k])), len(body))
-            loops.append(body[i:j])
-    return max(loops, key=lambda lp: sum("v_mfma" in l for l in lp))
+    blocks, cur = [], None        # [name, header it belongs to (or None), lines]
+    for line in lines[start:end]:
+        m = re.match(r"^(\.LBB\d+_\d+):|^; (%bb\.\d+):", line)
+        if m:
+            h = re.search(r"Loop: Header=(BB\d+_\d+) Depth=2", line)
+            cur = [re.sub(r"^\.L", "", m.group(1) or m.group(2)), h.group(1) if h else None, []]
+            if "Loop Header: Depth=2" in line:
+                cur[1] = cur[0]
+            blocks.append(cur)
+        elif cur is not None:
+            if "Loop Header: Depth=2" in line:
+                cur[1] = cur[0]
+            cur[2].append(line)
+    loops = {}
+    for name, header, body in blocks:
+        if header:
+            loops.setdefault(header, []).append((name, body))
+    header, best = max(loops.items(),
+                       key=lambda hb: sum("v_mfma" in l for _, b in hb[1] for l in b))
+    names = [n for n, _ in best]
+    k = names.index(header) if header in names else 0
+    order = best[k:] + best[:k]
+    return [l for _, b in order for l in b]
 
 
 def _read_to_use(loop):
@@ -126,9 +143,10 @@ def asm(stats):
     return _assembly()
 
 
-@pytest.mark.parametrize("gateup", [1, 0])
-def test_256_row_stage_loop_hides_lds_latency(asm, gateup):
-    loop = _stage_loop(asm, f"moe_tile_kernelILi256ELb{gateup}")
-    assert sum("v_mfma" in l for l in loop) == 64   # 2 k-steps x 8 x 4 fragments per wavefront
+@pytest.mark.parametrize("bm,gateup", [(256, 1), (256, 0), (128, 1), (128, 0)])
+def test_prefill_stage_loops_hide_lds_latency(asm, bm, gateup):
+    loop = _stage_loop(asm, f"moe_tile_kernelILi{bm}ELb{gateup}")
+    # 2 k-steps per stage x (FM x FN) fragments per wavefront: 8 x 4 at 256 rows, 4 x 4 at 128
+    assert sum("v_mfma" in l for l in loop) == (64 if bm == 256 else 32)
     d = _read_to_use(loop)
     assert len(d) >= 24 and min(d) >= 6, sorted(d)
