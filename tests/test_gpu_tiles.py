@@ -67,3 +67,32 @@ def test_tile_heights_against_oracle(dev, tsm, bm):
     mean_rel = ((out - ref).abs().mean() / ref.abs().mean()).item()
     print(f"bm={bm} vs oracle: max_abs={max_abs:.3e} mean_rel={mean_rel:.3e}", flush=True)
     assert max_abs <= 2e-2 and mean_rel <= 5e-3
+
+
+@pytest.mark.parametrize("kind", ["skew_remote"])
+def test_tile_heights_skewed_with_remote_slots(dev, tsm, kind):
+    """Skewed routing (a hot expert spanning several tiles of every height, cold experts with a
+    few rows, so 256-row tiles run as half tiles) with a quarter of the experts owned by
+    another GPU (their slots' ids are -1: zero rows, no GEMM): all heights give the same bits,
+    the remote slots contribute nothing, and the result matches the oracle."""
+    H, I, E, k, T = 768, 384, 32, 4, 700
+    print(f"tile heights {kind} H={H} I={I} E={E} k={k} T={T}", flush=True)
+    x, gw, w13, w2 = make_layer(T, H, E, I, torch.bfloat16, seed=17, device=dev)
+    p13, p2 = tsm.pack_moe_weights(w13, w2)
+    bias = torch.zeros(E)
+    bias[3] = 6.0        # expert 3 in nearly every token's top-k
+    bias[11] = 3.0
+    emap = torch.arange(E, dtype=torch.int64)
+    emap[24:] = -1       # experts 24..31 live on another GPU
+    w, ids, _ = tsm.moe_router(x, gw, k, True, emap.to(dev), bias.to(dev))
+    c = torch.bincount(ids.cpu().long().flatten() + 1, minlength=E + 1)
+    assert c[0] > 0 and c[1 + 3] > 512 and (c[1:][c[1:] > 0] < 128).any()  # remote, hot, cold
+    outs = {bm: staged(tsm, x, p13, p2, w, ids, E, I, bm) for bm in (64, 128, 256)}
+    assert torch.equal(outs[64], outs[128]), "64 vs 128"
+    assert torch.equal(outs[128], outs[256]), "128 vs 256"
+    ref = moe_reference(x.cpu(), w13.cpu(), w2.cpu(), w.cpu(), ids.cpu().long()).float()
+    out = outs[256].float().cpu()
+    max_abs = (out - ref).abs().max().item()
+    mean_rel = ((out - ref).abs().mean() / ref.abs().mean()).item()
+    print(f"{kind} vs oracle: max_abs={max_abs:.3e} mean_rel={mean_rel:.3e}", flush=True)
+    assert max_abs <= 2e-2 and mean_rel <= 5e-3
