@@ -262,8 +262,7 @@ __global__ __launch_bounds__(64 * kNW, 1) void moe_tile_kernel(GemmArgs p) {
             __builtin_amdgcn_global_load_lds(
                 BM == 256 ? (const void*)((const char*)ab + (uint32_t)(a_src[j] * 2u + st * 128u))
                           : (const void*)(a_base + a_src[j] + st * 64),
-                                             (lds_void*)(base + (wave + j * kNW) * kBlk), 16, 0,
-                                             0);
+                (lds_void*)(base + (wave + j * kNW) * kBlk), 16, 0, 0);
     };
     auto issue_b = [&](int st) {
         char* base = lds + 2 * A_BYTES + (st % NB) * B_BYTES;
@@ -353,9 +352,9 @@ __global__ __launch_bounds__(64 * kNW, 1) void moe_tile_kernel(GemmArgs p) {
         return __builtin_amdgcn_readlane(k < 64 ? remap0 : remap1, k & 63);
     };
 
-    // the halves of the A fragments (f = h * FM/2 + i) and the B fragments of one k-step
+    // the halves of the A fragments (f = h * FM/2 + i) and the B fragments of one k-step, from
     // per-lane read bases with the wavefront's block offsets folded in, so that the fragment
-    // offsets below are compile-time constants (immediate offsets of the LDS reads)
+    // offsets are compile-time constants (immediate offsets of the LDS reads)
     const uint32_t a_rd0 = lds0 + a_off[0] + wm * FM * 2 * kBlk;
     const uint32_t a_rd1 = lds0 + a_off[1] + wm * FM * 2 * kBlk;
     const uint32_t b_rd = lds0 + 2 * A_BYTES + lane * 16 + wn * FN * 2 * kBlk;
