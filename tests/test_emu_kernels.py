@@ -154,6 +154,29 @@ def test_autotune_small_layer(tsm, packed):
     assert {T: kernels.moe_block_m(T, H, I, E, k, packed) for T in (1, 40, 300)} == before
 
 
+def test_autotune_never_installs_a_disagreeing_plan(tsm, monkeypatch):
+    """A plan whose results disagree with the static plan's (here the 16-row plan, made wrong
+    on purpose on the host) is timed out of the table with a warning, whatever its speed."""
+    from tinyserve_amd import kernels
+    H, E, I, k = 256, 8, 512, 2
+    _, _, w13, w2 = make_layer(8, H, E, I, torch.bfloat16, seed=6)
+    real = kernels.fused_moe
+
+    def wrong_at_16(x, w13_, w2_, w, ids, sum_topk=True):
+        out = real(x, w13_, w2_, w, ids, sum_topk)
+        if kernels.moe_block_m(x.shape[0], H, I, E, k, False) == 16:
+            out = out + 1.0
+        return out
+
+    monkeypatch.setattr(kernels, "fused_moe", wrong_at_16)
+    try:
+        with pytest.warns(UserWarning, match="16-row plan disagrees"):
+            table = kernels.autotune_fused_moe(w13, w2, k, 64, packed=False, reps=1)
+        assert table and all(bm != 16 for bm, _ in table.values()), table
+    finally:
+        kernels.set_moe_block_m(1, 1 << 30, -1, False)
+
+
 def test_expert_parallel_and_rows(tsm):
     H, E, I, k, T = 256, 16, 128, 4, 50
     x, gw, w13, w2 = make_layer(T, H, E, I, torch.bfloat16, seed=3)

@@ -14,6 +14,8 @@ autotune_fused_moe times the kernel families and tile heights this build has (ex
 counts and installs the fastest in the library's plan table (set_moe_block_m). 256-row tiles
 exist only through it: the static table never picks them.
 """
+import warnings
+
 import torch
 
 from . import ops
@@ -57,6 +59,17 @@ def set_moe_block_m(numel_lo: int, numel_hi: int, block_m: int, packed: bool = F
     check(lib.tsm_moe_set_block_m(numel_lo, numel_hi, int(packed), block_m), "set_moe_block_m")
 
 
+def _agrees(out: torch.Tensor, ref: torch.Tensor) -> bool:
+    """Two plans' results of one layer agree: finite, and within the bf16 layer tolerance
+    (max-abs 2e-2 and mean relative 5e-3, relative to the result's own scale)."""
+    if not bool(torch.isfinite(out).all()):
+        return False
+    d = (out.float() - ref.float()).abs()
+    scale = ref.float().abs()
+    return (d.max().item() <= 2e-2 * max(1.0, scale.max().item())
+            and d.mean().item() <= 5e-3 * max(scale.mean().item(), 1e-30))
+
+
 def _candidates(numel: int, E: int, packed: bool):
     c = [16, 64] + ([128] if packed else [])
     if packed and numel > 32 * E:   # 256-row tiles: only where experts average > 32 rows
@@ -73,7 +86,9 @@ def autotune_fused_moe(w13: torch.Tensor, w2: torch.Tensor, top_k: int, max_num_
     max_num_tokens (random routing on the real expert weights, as the reference tunes,
     tinykernels.py:1798-1811) and install the fastest for each power-of-two bucket of
     assignment counts. `packed`: w13/w2 are pack_moe_weights output and the packed-layout plans
-    are tuned. Returns {numel bucket start: (block_m, microseconds)}."""
+    are tuned. Every candidate's output is first checked against the static plan's on the same
+    input; a plan that disagrees (beyond the bf16 tolerance of a layer) is never installed, and
+    a warning names it. Returns {numel bucket start: (block_m, microseconds)}."""
     fn = ops.fused_moe_packed if packed else fused_moe
     E, H = w13.shape[0], w13.shape[2]
     dev = w13.device
@@ -91,11 +106,17 @@ def autotune_fused_moe(w13: torch.Tensor, w2: torch.Tensor, top_k: int, max_num_
         ids = torch.randint(0, E, (T, top_k), device=dev, dtype=torch.int32)
         weights = torch.rand(T, top_k, device=dev)
         best = None
+        set_moe_block_m(numel, numel, -1, packed)
+        ref = fn(x, w13, w2, weights, ids)   # the static plan's result: what tuning must keep
         for bm in _candidates(numel, E, packed):
             set_moe_block_m(numel, numel, bm, packed)
             if moe_block_m(T, H, w2.shape[-1], E, top_k, packed) != bm:
                 continue   # the shape has no kernel at this height
-            fn(x, w13, w2, weights, ids)  # warm-up
+            out = fn(x, w13, w2, weights, ids)  # warm-up, and the check
+            if not _agrees(out, ref):
+                warnings.warn(f"autotune_fused_moe: the {bm}-row plan disagrees with the static "
+                              f"plan at T={T}; not installed")
+                continue
             start.record()
             for _ in range(reps):
                 fn(x, w13, w2, weights, ids)
