@@ -41,8 +41,8 @@ def staged(tsm, x, p13, p2, w, ids, E, I, bm):
     return out
 
 
-@pytest.mark.parametrize("H,I,E,k,T", [(2048, 768, 128, 8, 2048), (1024, 2816, 16, 2, 1500),
-                                       (768, 384, 32, 4, 700)])
+@pytest.mark.parametrize("H,I,E,k,T", [(2048, 768, 128, 8, 2048), (2048, 768, 128, 8, 1024),
+                                       (1024, 2816, 16, 2, 1500), (768, 384, 32, 4, 700)])
 def test_tile_heights_agree(dev, tsm, H, I, E, k, T):
     print(f"tile heights H={H} I={I} E={E} k={k} T={T}", flush=True)
     x, gw, w13, w2 = make_layer(T, H, E, I, torch.bfloat16, seed=T + E, device=dev)
